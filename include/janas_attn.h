@@ -1,0 +1,177 @@
+/*
+ * janas_attn.h - KV-cache attention on an MI355X (gfx950), C ABI.
+ *
+ * Part 1 is a drop-in for the engine's attention header
+ * (/root/reference/src/llm/attention.h): the same twelve entry points with
+ * the same meaning, so src/llm/model_attn.c and model_assist.c link against
+ * libjanas_attn.so unchanged. The cache contract is the reference's: keys
+ * and values n_head_kv x n_ctx x head_dim signed bytes (sixteen-bit with
+ * janas_attn_set_kv16), one float scale per (KV head, position), position p
+ * in row p (or p mod n_ctx in a ring). Pointers may be device memory (used
+ * in place) or host memory (staged through the device each call; correct,
+ * but bounded by PCIe - keep the cache in device memory).
+ *
+ * Part 2 extends it for callers that keep everything on the device: f16
+ * and f32 caches besides int8 / int16, any number of tokens a call, several
+ * sequences a call (each its own cache), the output gate fused, and an
+ * asynchronous stream. It has no counterpart in the reference header.
+ *
+ * Errors. janas_attn_create returns NULL on a geometry the reference
+ * rejects (attention.c:998-1000) or when the device cannot be used.
+ * janas_attn_run is void, as the reference's: a call the reference would
+ * abort on (a ring too small, attention.c:1281-1286) aborts with a message,
+ * and so does a device failure - there is no CPU path behind it to fall
+ * back on. The Part 2 entry points return 0 or a negative JANAS_ATTN_E*
+ * code and never abort.
+ */
+#ifndef JANAS_ATTN_HIP_H
+#define JANAS_ATTN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===== Part 1: the reference's interface (attention.h:26-112) ======== */
+
+/* attention.h:26 - tokens a janas_attn_run call takes */
+#define JANAS_ATTN_MAX_BLOCK 64
+
+/* attention.h:43-47. The device computes every score over the float query
+   (FLOAT, the reference's exact path): INT16 is a CPU instruction-set
+   speed-up, and asking for it gets FLOAT, which janas_attn_scores_mode
+   reports - as the reference itself does where INT16 cannot run
+   (attention.c:965-982, :1061-1066). */
+enum janas_attn_scores {
+    JANAS_ATTN_AUTO = 0,
+    JANAS_ATTN_FLOAT = 1,
+    JANAS_ATTN_INT16 = 2
+};
+
+struct janas_attn;
+/* the engine's thread pool (src/common/pool.h:14): accepted, not used */
+struct janas_pool;
+
+/* attention.h:58-59 - device bytes of the partials an instance keeps for
+   n_ctx positions (the same count as the reference's host partials). */
+size_t janas_attn_part_bytes(uint32_t n_head, uint32_t n_head_kv,
+                             uint32_t head_dim, uint32_t n_ctx);
+
+/* attention.h:62-64 - NULL on a bad geometry (n_head_kv 0, n_head not a
+   multiple of it, head_dim not a multiple of 8 or above 512, n_threads < 1),
+   when the device lacks memory, or when no device is there. head_dim above
+   256 is accepted by the reference and rejected here for now (NULL). */
+struct janas_attn *janas_attn_create(uint32_t n_head, uint32_t n_head_kv,
+                                     uint32_t head_dim, uint32_t n_ctx,
+                                     int n_threads, int scores);
+/* attention.h:65 */
+void janas_attn_destroy(struct janas_attn *a);
+
+/* attention.h:67-69 - 1 / sqrt(head_dim) until set */
+void janas_attn_set_scale(struct janas_attn *a, float scale);
+/* attention.h:70-72 - token p sees p - window + 1 .. p; 0: all */
+void janas_attn_set_window(struct janas_attn *a, uint32_t window);
+/* attention.h:73-76 - int16 keys and values with the same scales */
+void janas_attn_set_kv16(struct janas_attn *a, int on);
+/* attention.h:77-84 - position p in row p mod n_ctx (n_ctx a multiple of
+   256); a call must fit (janas_attn_ring_positions) */
+void janas_attn_set_ring(struct janas_attn *a, int on);
+/* attention.h:85-87 */
+uint32_t janas_attn_ring_positions(uint32_t window, uint32_t n);
+/* attention.h:89-97 - for the next call only: token j sees up to last[j]
+   (host array, n entries, read during that call) */
+void janas_attn_set_last(struct janas_attn *a, const uint32_t *last);
+/* attention.h:99-102 */
+int janas_attn_scores_mode(const struct janas_attn *a);
+int janas_attn_scores_auto(const struct janas_attn *a);
+
+/* attention.h:104-112 - q, out: n x n_head x head_dim floats; k, v: the
+   layer's cache, ks, vs its scales. n <= JANAS_ATTN_MAX_BLOCK. Synchronous:
+   out is written when it returns. */
+void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
+                    const float *q, const int8_t *k, const float *ks,
+                    const int8_t *v, const float *vs, uint32_t n,
+                    uint32_t pos0, float *out);
+
+/* ===== Part 2: the device extension (no counterpart in the reference) = */
+
+enum janas_attn_kv {
+    JANAS_ATTN_KV_I8 = 0,  /* int8, float scale per (KV head, position) */
+    JANAS_ATTN_KV_I16 = 1, /* int16, the same scales */
+    JANAS_ATTN_KV_F16 = 2, /* IEEE half, no scales */
+    JANAS_ATTN_KV_F32 = 3  /* float, no scales */
+};
+
+enum janas_attn_gate {
+    JANAS_ATTN_GATE_NONE = 0,
+    JANAS_ATTN_GATE_ELEM = 1, /* out *= sigmoid(g), g n x n_head x head_dim */
+    JANAS_ATTN_GATE_HEAD = 2  /* g n x n_head, one gate a head */
+};
+
+enum janas_attn_err {
+    JANAS_ATTN_OK = 0,
+    JANAS_ATTN_EINVAL = -1,  /* bad arguments */
+    JANAS_ATTN_ERANGE = -2,  /* positions past the cache, a ring too small */
+    JANAS_ATTN_ENOMEM = -3,  /* device memory */
+    JANAS_ATTN_EDEVICE = -4, /* a HIP call failed */
+    JANAS_ATTN_ENOTSUP = -5  /* no kernel for this element type / size */
+};
+
+/* One sequence of a call. Every pointer is a device address. */
+struct janas_attn_seq {
+    const void *k, *v;    /* n_head_kv x cap x head_dim elements */
+    const float *ks, *vs; /* n_head_kv x cap, int8 / int16 caches only */
+    const float *q;       /* n x n_head x head_dim */
+    float *out;           /* n x n_head x head_dim */
+    const float *gate;    /* per the call's gate mode, or NULL */
+    const uint32_t *last; /* n entries (set_last's meaning), or NULL */
+    uint32_t cap;         /* rows a KV head: the cache's n_ctx */
+    uint32_t n;           /* tokens */
+    uint32_t pos0;        /* position of the first */
+    uint32_t last_max;    /* with last: last[n - 1]; ignored otherwise */
+};
+
+/*
+ * Attention of n_seqs sequences on a stream (a hipStream_t; NULL: the
+ * instance's own), asynchronous. The instance's geometry, scale, window and
+ * ring apply to all. Blocks of up to JANAS_ATTN_MAX_BLOCK tokens a sequence
+ * take the split-KV path, whose chunking matches janas_attn_run bit for bit
+ * token by token; longer prompts take the MFMA prefill path (causal tiles,
+ * no partials), equal within the f16 tolerance. The instance's partials are
+ * grown as needed; one call at a time per instance.
+ */
+int janas_attn_run_dev(struct janas_attn *a, int kv_type, int gate_mode,
+                       const struct janas_attn_seq *seqs, uint32_t n_seqs,
+                       void *stream);
+
+/* The same, always through the split-KV path (any n). */
+int janas_attn_run_dev_split(struct janas_attn *a, int kv_type, int gate_mode,
+                             const struct janas_attn_seq *seqs,
+                             uint32_t n_seqs, void *stream);
+
+/* The same, always through the MFMA prefill path (f16 / int8 caches). */
+int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
+                               int gate_mode,
+                               const struct janas_attn_seq *seqs,
+                               uint32_t n_seqs, void *stream);
+
+/* A message for a JANAS_ATTN_E* code. */
+const char *janas_attn_strerror(int err);
+
+/*
+ * Kernel timing for measurement: while on, every launch of the instance is
+ * bracketed by HIP events on its stream; janas_attn_prof_read returns, per
+ * kernel (0 split, 1 merge, 2 prefill), the launches and their summed
+ * milliseconds (synchronizing the stream), and zeroes them.
+ */
+void janas_attn_prof_enable(struct janas_attn *a, int on);
+int janas_attn_prof_read(struct janas_attn *a, uint32_t counts[3],
+                         double ms[3]);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

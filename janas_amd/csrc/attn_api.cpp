@@ -1,0 +1,673 @@
+/*
+ * attn_api.cpp - the C ABI of include/janas_attn.h over the HIP kernels.
+ *
+ * The instance mirrors the reference's struct janas_attn
+ * (src/llm/attention.c:37-58): geometry, scale, window, ring, sixteen-bit
+ * cache, the next call's last positions; what the reference keeps in host
+ * memory (partials) lives on the device, with the stream the calls run on.
+ */
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/janas_attn.h"
+#include "attn_kernels.h"
+
+using namespace janas;
+
+namespace {
+
+struct ProfEv {
+    int kind;
+    hipEvent_t a, b;
+};
+
+}  // namespace
+
+struct janas_attn {
+    uint32_t n_head, n_kv, hd, n_ctx, group;
+    int scores_auto;
+    float scale;
+    uint32_t window;
+    int kv16, ring;
+    const uint32_t *last; /* host, the next janas_attn_run only */
+    int dev;
+    hipStream_t stream;
+    /* partials: part_rows rows of (m, l) and of hd values */
+    float *part_ml, *part_acc;
+    uint64_t part_rows;
+    /* staging of host pointers for janas_attn_run */
+    float *st_q, *st_out;
+    void *st_k, *st_v;
+    float *st_ks, *st_vs;
+    uint32_t *st_last;
+    /* timing */
+    int prof;
+    std::vector<ProfEv> *ev_used, *ev_free;
+};
+
+namespace {
+
+int hip_err(hipError_t e, const char *what)
+{
+    if (e == hipSuccess)
+        return JANAS_ATTN_OK;
+    fprintf(stderr, "janas_attn: %s: %s\n", what, hipGetErrorString(e));
+    return JANAS_ATTN_EDEVICE;
+}
+
+bool is_device_ptr(const void *p)
+{
+    if (!p)
+        return false;
+    hipPointerAttribute_t at;
+    hipError_t e = hipPointerGetAttributes(&at, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError(); /* an unregistered host pointer */
+        return false;
+    }
+    return at.type == hipMemoryTypeDevice || at.type == hipMemoryTypeManaged;
+}
+
+uint32_t elem_bytes(int kv)
+{
+    return kv == kI8 ? 1 : kv == kF32 ? 4 : 2;
+}
+
+uint32_t first_chunk(uint32_t window, uint32_t pos0)
+{
+    return window && pos0 + 1 > window ? (pos0 + 1 - window) / kChunk : 0;
+}
+
+/* Fill the kernel view of one sequence and check it against the cache. */
+int describe(const janas_attn *a, int kv, const janas_attn_seq &s, SeqDesc &d)
+{
+    if (!s.k || !s.v || !s.q || !s.out || s.n == 0 || s.cap == 0)
+        return JANAS_ATTN_EINVAL;
+    if ((kv == kI8 || kv == kI16) && (!s.ks || !s.vs))
+        return JANAS_ATTN_EINVAL;
+    memset(&d, 0, sizeof d);
+    d.k = s.k;
+    d.v = s.v;
+    d.ks = s.ks;
+    d.vs = s.vs;
+    d.q = s.q;
+    d.out = s.out;
+    d.gate = s.gate;
+    d.last = s.last;
+    d.cap = s.cap;
+    d.n = s.n;
+    d.pos0 = s.pos0;
+    if (s.last && s.last_max < s.pos0 + s.n - 1)
+        return JANAS_ATTN_EINVAL;
+    uint64_t end = s.last ? (uint64_t)s.last_max + 1 : (uint64_t)s.pos0 + s.n;
+    if (end > 0xFFFFFF00u)
+        return JANAS_ATTN_ERANGE;
+    d.end = (uint32_t)end;
+    d.c0 = first_chunk(a->window, s.pos0);
+    uint32_t n_chunks = (d.end + kChunk - 1) / kChunk;
+    d.span = n_chunks - d.c0;
+    if (a->ring) {
+        /* attention.c:1281-1286: the call must fit in the ring */
+        if (s.cap % kChunk || d.span * kChunk > s.cap)
+            return JANAS_ATTN_ERANGE;
+    } else if (d.end > s.cap) {
+        return JANAS_ATTN_ERANGE;
+    }
+    d.rtiles = (s.n * a->group + 15) / 16;
+    return JANAS_ATTN_OK;
+}
+
+int ensure_part(janas_attn *a, uint64_t rows, hipStream_t stream)
+{
+    if (rows <= a->part_rows)
+        return JANAS_ATTN_OK;
+    /* the stream may still read the old ones */
+    if (a->part_ml || a->part_acc) {
+        hipError_t e = hipStreamSynchronize(stream);
+        if (e != hipSuccess)
+            return hip_err(e, "synchronize");
+        (void)hipFree(a->part_ml);
+        (void)hipFree(a->part_acc);
+        a->part_ml = a->part_acc = nullptr;
+        a->part_rows = 0;
+    }
+    if (hipMalloc(&a->part_ml, rows * 2 * sizeof(float)) != hipSuccess ||
+        hipMalloc(&a->part_acc, rows * a->hd * sizeof(float)) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(a->part_ml);
+        (void)hipFree(a->part_acc);
+        a->part_ml = a->part_acc = nullptr;
+        return JANAS_ATTN_ENOMEM;
+    }
+    a->part_rows = rows;
+    return JANAS_ATTN_OK;
+}
+
+ProfEv *prof_begin(janas_attn *a, int kind, hipStream_t stream)
+{
+    if (!a->prof)
+        return nullptr;
+    ProfEv ev;
+    if (!a->ev_free->empty()) {
+        ev = a->ev_free->back();
+        a->ev_free->pop_back();
+    } else if (hipEventCreate(&ev.a) != hipSuccess ||
+               hipEventCreate(&ev.b) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    ev.kind = kind;
+    a->ev_used->push_back(ev);
+    (void)hipEventRecord(a->ev_used->back().a, stream);
+    return &a->ev_used->back();
+}
+
+void prof_end(ProfEv *ev, hipStream_t stream)
+{
+    if (ev)
+        (void)hipEventRecord(ev->b, stream);
+}
+
+int fill_args(const janas_attn *a, SplitArgs &args, int gate_mode)
+{
+    args.part_ml = a->part_ml;
+    args.part_acc = a->part_acc;
+    args.n_head = a->n_head;
+    args.n_kv = a->n_kv;
+    args.group = a->group;
+    args.hd = a->hd;
+    args.window = a->window;
+    args.scale = a->scale;
+    args.ring = a->ring;
+    args.gate_mode = gate_mode;
+    return JANAS_ATTN_OK;
+}
+
+int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
+              uint32_t n_seqs, hipStream_t stream)
+{
+    if (!split_supported(kv, a->hd))
+        return JANAS_ATTN_ENOTSUP;
+    for (uint32_t s0 = 0; s0 < n_seqs; s0 += kMaxSeqs) {
+        uint32_t m = std::min(kMaxSeqs, n_seqs - s0);
+        SplitArgs args;
+        memset(&args, 0, sizeof args);
+        uint64_t rows = 0;
+        uint32_t wg = 0, mg = 0, nd = (a->hd + 63) / 64;
+        for (uint32_t i = 0; i < m; i++) {
+            SeqDesc &d = args.seq[i];
+            int rc = describe(a, kv, seqs[s0 + i], d);
+            if (rc)
+                return rc;
+            d.wg0 = wg;
+            d.mg0 = mg;
+            d.part0 = rows;
+            uint64_t nwg = (uint64_t)a->n_kv * d.span * d.rtiles;
+            uint64_t nmg = (uint64_t)d.n * a->n_head * nd;
+            if (wg + nwg > 0x7FFFFFFFu || mg + nmg > 0x7FFFFFFFu)
+                return JANAS_ATTN_ERANGE;
+            wg += (uint32_t)nwg;
+            mg += (uint32_t)nmg;
+            rows += (uint64_t)a->n_kv * d.span * d.n * a->group;
+        }
+        int rc = ensure_part(a, rows, stream);
+        if (rc)
+            return rc;
+        args.n_seqs = m;
+        args.n_wg = wg;
+        fill_args(a, args, gate_mode);
+        ProfEv *ev = prof_begin(a, 0, stream);
+        hipError_t e = launch_split(kv, args, stream);
+        prof_end(ev, stream);
+        if (e != hipSuccess)
+            return hip_err(e, "split launch");
+        ev = prof_begin(a, 1, stream);
+        e = launch_merge(args, mg, stream);
+        prof_end(ev, stream);
+        if (e != hipSuccess)
+            return hip_err(e, "merge launch");
+    }
+    return JANAS_ATTN_OK;
+}
+
+int run_prefill(janas_attn *a, int kv, int gate_mode,
+                const janas_attn_seq *seqs, uint32_t n_seqs, hipStream_t stream)
+{
+    if (!prefill_supported(kv, a->hd))
+        return JANAS_ATTN_ENOTSUP;
+    uint32_t bt = prefill_block_tokens(a->group);
+    for (uint32_t s0 = 0; s0 < n_seqs; s0 += kMaxSeqs) {
+        uint32_t m = std::min(kMaxSeqs, n_seqs - s0);
+        PrefillArgs args;
+        memset(&args, 0, sizeof args);
+        uint32_t wg = 0;
+        for (uint32_t i = 0; i < m; i++) {
+            SeqDesc &d = args.seq[i];
+            int rc = describe(a, kv, seqs[s0 + i], d);
+            if (rc)
+                return rc;
+            d.wg0 = wg;
+            uint64_t nwg = (uint64_t)a->n_kv * ((d.n + bt - 1) / bt);
+            if (wg + nwg > 0x7FFFFFFFu)
+                return JANAS_ATTN_ERANGE;
+            wg += (uint32_t)nwg;
+        }
+        args.n_seqs = m;
+        args.n_wg = wg;
+        args.n_head = a->n_head;
+        args.n_kv = a->n_kv;
+        args.group = a->group;
+        args.hd = a->hd;
+        args.window = a->window;
+        args.scale = a->scale;
+        args.ring = a->ring;
+        args.gate_mode = gate_mode;
+        ProfEv *ev = prof_begin(a, 2, stream);
+        hipError_t e = launch_prefill(kv, args, stream);
+        prof_end(ev, stream);
+        if (e != hipSuccess)
+            return hip_err(e, "prefill launch");
+    }
+    return JANAS_ATTN_OK;
+}
+
+int check_call(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
+               uint32_t n_seqs)
+{
+    if (!a || !seqs || n_seqs == 0 || kv < kI8 || kv > kF32 ||
+        gate_mode < kGateNone || gate_mode > kGateHead)
+        return JANAS_ATTN_EINVAL;
+    for (uint32_t i = 0; i < n_seqs; i++)
+        if (gate_mode != kGateNone && !seqs[i].gate)
+            return JANAS_ATTN_EINVAL;
+    hipError_t e = hipSetDevice(a->dev);
+    return e == hipSuccess ? JANAS_ATTN_OK : hip_err(e, "set device");
+}
+
+[[noreturn]] void die(const char *what, int rc)
+{
+    fprintf(stderr, "janas_attn_run: %s (%s)\n", what,
+            janas_attn_strerror(rc));
+    abort();
+}
+
+}  // namespace
+
+/* ===== Part 1 ========================================================= */
+
+extern "C" size_t janas_attn_part_bytes(uint32_t n_head, uint32_t n_head_kv,
+                                        uint32_t head_dim, uint32_t n_ctx)
+{
+    /* attention.c:984-992 */
+    if (n_head_kv == 0)
+        return 0;
+    size_t chunks = (n_ctx + kChunk - 1) / kChunk;
+    return (size_t)n_head_kv * chunks * JANAS_ATTN_MAX_BLOCK *
+           (n_head / n_head_kv) * (head_dim + 2) * sizeof(float);
+}
+
+extern "C" struct janas_attn *janas_attn_create(uint32_t n_head,
+                                                uint32_t n_head_kv,
+                                                uint32_t head_dim,
+                                                uint32_t n_ctx, int n_threads,
+                                                int scores)
+{
+    /* attention.c:998-1000 */
+    if (n_head_kv == 0 || n_head % n_head_kv || head_dim % 8 ||
+        head_dim > 512 || n_threads < 1)
+        return nullptr;
+    if (head_dim > 256)
+        return nullptr; /* no kernel instance yet */
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    janas_attn *a = (janas_attn *)calloc(1, sizeof(janas_attn));
+    if (!a)
+        return nullptr;
+    a->n_head = n_head;
+    a->n_kv = n_head_kv;
+    a->hd = head_dim;
+    a->n_ctx = n_ctx;
+    a->group = n_head / n_head_kv;
+    a->dev = dev;
+    a->scale = 1.0f / sqrtf((float)head_dim);
+    /* attention.c:965-982: JANAS_ATTN overrides the asked way */
+    const char *e = getenv("JANAS_ATTN");
+    if (e && !strcmp(e, "float"))
+        scores = JANAS_ATTN_FLOAT;
+    else if (e && !strcmp(e, "int16"))
+        scores = JANAS_ATTN_INT16;
+    else if (e && !strcmp(e, "auto"))
+        scores = JANAS_ATTN_AUTO;
+    a->scores_auto = scores == JANAS_ATTN_AUTO;
+    a->ev_used = new std::vector<ProfEv>();
+    a->ev_free = new std::vector<ProfEv>();
+    if (hipStreamCreateWithFlags(&a->stream, hipStreamNonBlocking) !=
+        hipSuccess) {
+        (void)hipGetLastError();
+        a->stream = nullptr;
+        janas_attn_destroy(a);
+        return nullptr;
+    }
+    /* the partials of a full janas_attn_run block, as the reference
+       allocates them (attention.c:1013) */
+    uint32_t chunks = (n_ctx + kChunk - 1) / kChunk;
+    uint64_t rows = (uint64_t)n_head_kv * (chunks ? chunks : 1) *
+                    JANAS_ATTN_MAX_BLOCK * a->group;
+    if (ensure_part(a, rows, a->stream) != JANAS_ATTN_OK) {
+        janas_attn_destroy(a);
+        return nullptr;
+    }
+    return a;
+}
+
+extern "C" void janas_attn_destroy(struct janas_attn *a)
+{
+    if (!a)
+        return;
+    (void)hipSetDevice(a->dev);
+    if (a->stream)
+        (void)hipStreamSynchronize(a->stream);
+    (void)hipFree(a->part_ml);
+    (void)hipFree(a->part_acc);
+    (void)hipFree(a->st_q);
+    (void)hipFree(a->st_out);
+    (void)hipFree(a->st_k);
+    (void)hipFree(a->st_v);
+    (void)hipFree(a->st_ks);
+    (void)hipFree(a->st_vs);
+    (void)hipFree(a->st_last);
+    for (std::vector<ProfEv> *v : {a->ev_used, a->ev_free})
+        if (v) {
+            for (ProfEv &ev : *v) {
+                (void)hipEventDestroy(ev.a);
+                (void)hipEventDestroy(ev.b);
+            }
+            delete v;
+        }
+    if (a->stream)
+        (void)hipStreamDestroy(a->stream);
+    free(a);
+}
+
+extern "C" void janas_attn_set_scale(struct janas_attn *a, float scale)
+{
+    a->scale = scale;
+}
+
+extern "C" void janas_attn_set_window(struct janas_attn *a, uint32_t window)
+{
+    a->window = window;
+}
+
+extern "C" void janas_attn_set_kv16(struct janas_attn *a, int on)
+{
+    a->kv16 = on != 0;
+}
+
+extern "C" void janas_attn_set_ring(struct janas_attn *a, int on)
+{
+    a->ring = on != 0;
+}
+
+extern "C" uint32_t janas_attn_ring_positions(uint32_t window, uint32_t n)
+{
+    /* attention.c:1048-1054: the window, the tokens and a chunk for the
+       first token's alignment, in whole chunks */
+    uint32_t need = window + n + kChunk;
+    return (need + kChunk - 1) / kChunk * kChunk;
+}
+
+extern "C" void janas_attn_set_last(struct janas_attn *a, const uint32_t *last)
+{
+    a->last = last;
+}
+
+extern "C" int janas_attn_scores_mode(const struct janas_attn *a)
+{
+    (void)a;
+    return JANAS_ATTN_FLOAT;
+}
+
+extern "C" int janas_attn_scores_auto(const struct janas_attn *a)
+{
+    return a ? a->scores_auto : 0;
+}
+
+extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
+                               const float *q, const int8_t *k,
+                               const float *ks, const int8_t *v,
+                               const float *vs, uint32_t n, uint32_t pos0,
+                               float *out)
+{
+    (void)pool;
+    const uint32_t *last = a->last;
+    a->last = nullptr; /* one call only (attention.c:1270-1272) */
+    if (n == 0)
+        return;
+    if (n > JANAS_ATTN_MAX_BLOCK)
+        die("more tokens than JANAS_ATTN_MAX_BLOCK", JANAS_ATTN_EINVAL);
+    if (hipSetDevice(a->dev) != hipSuccess)
+        die("set device", JANAS_ATTN_EDEVICE);
+    const int kv = a->kv16 ? kI16 : kI8;
+    const size_t eb = elem_bytes(kv), hd = a->hd, cap = a->n_ctx;
+    const size_t qbytes = (size_t)n * a->n_head * hd * sizeof(float);
+    uint32_t end = last ? last[n - 1] + 1 : pos0 + n;
+    if (!a->ring && end > cap)
+        die("positions past the cache", JANAS_ATTN_ERANGE);
+    uint32_t c0 = first_chunk(a->window, pos0);
+    if (a->ring && ((end + kChunk - 1) / kChunk - c0) * kChunk > cap) {
+        fprintf(stderr, "janas_attn_run: %u chunks for a ring of %u\n",
+                (end + kChunk - 1) / kChunk - c0, (uint32_t)(cap / kChunk));
+        abort();
+    }
+    int rc = JANAS_ATTN_OK;
+    janas_attn_seq s;
+    memset(&s, 0, sizeof s);
+    s.cap = a->n_ctx;
+    s.n = n;
+    s.pos0 = pos0;
+    /* q and out: in place on the device, else through a block's buffer */
+    const size_t blk_bytes =
+        (size_t)JANAS_ATTN_MAX_BLOCK * a->n_head * hd * sizeof(float);
+    if (is_device_ptr(q)) {
+        s.q = q;
+    } else {
+        if (!a->st_q && hipMalloc(&a->st_q, blk_bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            die("staging q", JANAS_ATTN_ENOMEM);
+        }
+        rc = hip_err(hipMemcpyAsync(a->st_q, q, qbytes, hipMemcpyHostToDevice,
+                                    a->stream),
+                     "copy q");
+        if (rc)
+            die("staging q", rc);
+        s.q = a->st_q;
+    }
+    const bool out_host = !is_device_ptr(out);
+    if (out_host) {
+        if (!a->st_out && hipMalloc(&a->st_out, blk_bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            die("staging out", JANAS_ATTN_ENOMEM);
+        }
+        s.out = a->st_out;
+    } else {
+        s.out = out;
+    }
+    /* the cache: in place on the device, else the rows this call reads */
+    const size_t rows_all = (size_t)a->n_kv * cap;
+    const size_t kv_bytes = rows_all * hd * eb, sc_bytes = rows_all * 4;
+    size_t r_lo = a->ring ? 0 : (size_t)c0 * kChunk;
+    size_t r_hi = a->ring ? cap : end;
+    struct Src {
+        const void *p;
+        void **st;
+        size_t bytes, esz;
+        const void **dst;
+    } src[4] = {{k, &a->st_k, kv_bytes, hd * eb, &s.k},
+                {v, &a->st_v, kv_bytes, hd * eb, &s.v},
+                {ks, (void **)&a->st_ks, sc_bytes, 4, (const void **)&s.ks},
+                {vs, (void **)&a->st_vs, sc_bytes, 4, (const void **)&s.vs}};
+    for (Src &x : src) {
+        if (is_device_ptr(x.p)) {
+            *x.dst = x.p;
+            continue;
+        }
+        if (!*x.st) {
+            if (hipMalloc(x.st, x.bytes) != hipSuccess) {
+                (void)hipGetLastError();
+                die("staging the cache", JANAS_ATTN_ENOMEM);
+            }
+        }
+        /* per KV head, rows r_lo .. r_hi - 1 */
+        size_t pitch = cap * x.esz, width = (r_hi - r_lo) * x.esz;
+        const char *sp = (const char *)x.p + r_lo * x.esz;
+        char *dp = (char *)*x.st + r_lo * x.esz;
+        rc = hip_err(hipMemcpy2DAsync(dp, pitch, sp, pitch, width, a->n_kv,
+                                      hipMemcpyHostToDevice, a->stream),
+                     "copy cache rows");
+        if (rc)
+            die("staging the cache", rc);
+        *x.dst = *x.st;
+    }
+    if (last) {
+        if (!a->st_last &&
+            hipMalloc(&a->st_last, JANAS_ATTN_MAX_BLOCK * sizeof(uint32_t)) !=
+                hipSuccess) {
+            (void)hipGetLastError();
+            die("staging last", JANAS_ATTN_ENOMEM);
+        }
+        rc = hip_err(hipMemcpyAsync(a->st_last, last, n * sizeof(uint32_t),
+                                    hipMemcpyHostToDevice, a->stream),
+                     "copy last");
+        if (rc)
+            die("staging last", rc);
+        s.last = a->st_last;
+        s.last_max = last[n - 1];
+    }
+    rc = run_split(a, kv, kGateNone, &s, 1, a->stream);
+    if (rc)
+        die("attention", rc);
+    if (out_host) {
+        rc = hip_err(hipMemcpyAsync(out, a->st_out, qbytes,
+                                    hipMemcpyDeviceToHost, a->stream),
+                     "copy out");
+        if (rc)
+            die("copy out", rc);
+    }
+    rc = hip_err(hipStreamSynchronize(a->stream), "synchronize");
+    if (rc)
+        die("synchronize", rc);
+}
+
+/* ===== Part 2 ========================================================= */
+
+extern "C" int janas_attn_run_dev_split(struct janas_attn *a, int kv_type,
+                                        int gate_mode,
+                                        const struct janas_attn_seq *seqs,
+                                        uint32_t n_seqs, void *stream)
+{
+    int rc = check_call(a, kv_type, gate_mode, seqs, n_seqs);
+    if (rc)
+        return rc;
+    return run_split(a, kv_type, gate_mode, seqs, n_seqs,
+                     stream ? (hipStream_t)stream : a->stream);
+}
+
+extern "C" int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
+                                          int gate_mode,
+                                          const struct janas_attn_seq *seqs,
+                                          uint32_t n_seqs, void *stream)
+{
+    int rc = check_call(a, kv_type, gate_mode, seqs, n_seqs);
+    if (rc)
+        return rc;
+    return run_prefill(a, kv_type, gate_mode, seqs, n_seqs,
+                       stream ? (hipStream_t)stream : a->stream);
+}
+
+extern "C" int janas_attn_run_dev(struct janas_attn *a, int kv_type,
+                                  int gate_mode,
+                                  const struct janas_attn_seq *seqs,
+                                  uint32_t n_seqs, void *stream)
+{
+    int rc = check_call(a, kv_type, gate_mode, seqs, n_seqs);
+    if (rc)
+        return rc;
+    hipStream_t st = stream ? (hipStream_t)stream : a->stream;
+    /* blocks of up to JANAS_ATTN_MAX_BLOCK tokens keep the split-KV
+       chunking of janas_attn_run; longer prompts take the prefill tiles */
+    bool any_long = false;
+    for (uint32_t i = 0; i < n_seqs; i++)
+        any_long |= seqs[i].n > JANAS_ATTN_MAX_BLOCK;
+    if (any_long && prefill_supported(kv_type, a->hd)) {
+        std::vector<janas_attn_seq> shortq, longq;
+        for (uint32_t i = 0; i < n_seqs; i++)
+            (seqs[i].n > JANAS_ATTN_MAX_BLOCK ? longq : shortq).push_back(seqs[i]);
+        if (!shortq.empty()) {
+            rc = run_split(a, kv_type, gate_mode, shortq.data(),
+                           (uint32_t)shortq.size(), st);
+            if (rc)
+                return rc;
+        }
+        return run_prefill(a, kv_type, gate_mode, longq.data(),
+                           (uint32_t)longq.size(), st);
+    }
+    return run_split(a, kv_type, gate_mode, seqs, n_seqs, st);
+}
+
+extern "C" const char *janas_attn_strerror(int err)
+{
+    switch (err) {
+    case JANAS_ATTN_OK:
+        return "ok";
+    case JANAS_ATTN_EINVAL:
+        return "invalid argument";
+    case JANAS_ATTN_ERANGE:
+        return "positions outside the cache";
+    case JANAS_ATTN_ENOMEM:
+        return "out of device memory";
+    case JANAS_ATTN_EDEVICE:
+        return "device error";
+    case JANAS_ATTN_ENOTSUP:
+        return "no kernel for this element type or head size";
+    }
+    return "unknown error";
+}
+
+extern "C" void janas_attn_prof_enable(struct janas_attn *a, int on)
+{
+    a->prof = on != 0;
+}
+
+extern "C" int janas_attn_prof_read(struct janas_attn *a, uint32_t counts[3],
+                                    double ms[3])
+{
+    for (int i = 0; i < 3; i++) {
+        counts[i] = 0;
+        ms[i] = 0.0;
+    }
+    if (hipSetDevice(a->dev) != hipSuccess)
+        return JANAS_ATTN_EDEVICE;
+    for (ProfEv &ev : *a->ev_used) {
+        if (hipEventSynchronize(ev.b) != hipSuccess)
+            return hip_err(hipGetLastError(), "event");
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, ev.a, ev.b) != hipSuccess)
+            return hip_err(hipGetLastError(), "elapsed time");
+        counts[ev.kind]++;
+        ms[ev.kind] += t;
+        a->ev_free->push_back(ev);
+    }
+    a->ev_used->clear();
+    return JANAS_ATTN_OK;
+}
