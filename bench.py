@@ -1,0 +1,184 @@
+"""Benchmark of the KV-cache attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Headline (BASELINE.json metric): decode attention KV GB/s at 32k context on
+BASELINE config 4 - 16 query / 2 KV heads, head_dim 256, 32,768 positions,
+f16 K/V, f32 query, gate sigmoid(g) fused - and causal prefill TFLOPS at 8k
+(32 / 8 / 128, 8,192 tokens). A step is one attention call over the resident
+cache (the split kernel and the merge). Inputs are synthetic N(0, 1), drawn
+from a fixed seed, resident in HBM before timing starts.
+
+Prints one JSON line. ``roofline`` is the split kernel's: its algorithmic
+bytes (every K/V element of the visible positions once) over its average
+launch time, measured with HIP events on the stream it runs on, against the
+8 TB/s HBM peak. ``cpu_baseline`` times this repo's C restatement of the
+reference's CPU attention (oracle/, pthreads over the host's cores) on a
+bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = ("decode attn KV GB/s (% HBM peak) @32k ctx; "
+          "prefill attn TFLOPS (% MFMA peak) @8k")
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+SEED = 20261201
+
+
+def normal(rng, shape, dtype):
+    return rng.standard_normal(shape, dtype=np.float32).astype(dtype)
+
+
+def decode_workload():
+    """BASELINE config 4."""
+    h, kvh, hd, L = 16, 2, 256, 32768
+    rng = np.random.default_rng(SEED)
+    return dict(h=h, kvh=kvh, hd=hd, L=L, scale=1.0 / 16.0,
+                k=normal(rng, (kvh, L, hd), np.float16),
+                v=normal(rng, (kvh, L, hd), np.float16),
+                q=normal(rng, (1, h, hd), np.float32),
+                g=normal(rng, (1, h, hd), np.float32))
+
+
+def traffic_from_profiles(kernel):
+    """HBM bytes a launch from profiles/<kernel>_traffic.md (the PMC runs'
+    summary), or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_traffic.md")
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
+    return float(m.group(1)) if m else None
+
+
+def cpu_decode_baseline(w, budget_s=10.0):
+    """The restatement on the host's cores over the same config-4 call."""
+    from oracle import orc
+    cores = max(1, min(16, os.cpu_count() or 1))
+    args = dict(n_head=w["h"], n_kv=w["kvh"], hd=w["hd"], pos0=w["L"] - 1,
+                kv=orc.KV_F16, scale=w["scale"], threads=cores)
+    orc.run(w["q"], w["k"], w["v"], **args)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        out = orc.run(w["q"], w["k"], w["v"], **args)
+        orc.gate(out, w["g"])
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    kv_bytes = 2 * w["kvh"] * w["L"] * w["hd"] * 2
+    return {"value": round(kv_bytes / t / 1e9, 3), "unit": "GB/s",
+            "cores": cores, "kind": "port",
+            "sample": f"config 4 decode call (32768 positions), median of "
+                      f"{len(times)} calls, {t * 1e3:.1f} ms each"}
+
+
+def bench_decode(torch, jm, w, steps, warmup):
+    """Decode steps (split + merge kernels) launched back to back on one
+    stream; then the kernels' own launch times, bracketed by HIP events on
+    that stream."""
+    dev = torch.device("cuda:0")
+    k = torch.from_numpy(w["k"]).to(dev)
+    v = torch.from_numpy(w["v"]).to(dev)
+    q = torch.from_numpy(w["q"]).to(dev)
+    g = torch.from_numpy(w["g"]).to(dev)
+    out = torch.empty_like(q)
+    seq = [dict(k=k, v=v, q=q, out=out, gate=g, cap=w["L"], n=1,
+                pos0=w["L"] - 1)]
+    a = jm.Attention(w["h"], w["kvh"], w["hd"], w["L"])
+    a.set_scale(w["scale"])
+    stream = torch.cuda.current_stream()
+    step = a.prepare(jm.KV_F16, seq, gate_mode=jm.GATE_ELEM,
+                     stream=stream.cuda_stream, path="split")
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(
+        enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    a.prof_enable(True)
+    for _ in range(min(steps, 500)):
+        step()
+    prof = a.prof_read()
+    a.prof_enable(False)
+    a.close()
+    return ms, wall, prof
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is "
+              "not supported (the path's multi-GPU sharding is design only)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import janas_amd as jm
+    jm.lib()
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+
+    w = decode_workload()
+    ms, wall, prof = bench_decode(torch, jm, w, args.steps, args.warmup)
+    kv_bytes = 2 * w["kvh"] * w["L"] * w["hd"] * 2
+    value = kv_bytes / (ms * 1e-3) / 1e9
+    n_split, ms_split = prof["split"]
+    split_us = ms_split / max(1, n_split) * 1e3
+    achieved = kv_bytes / (split_us * 1e-6) / 1e9
+    n_merge, ms_merge = prof["merge"]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic N(0,1), seeded",
+        "config": {"workload": "BASELINE config 4: gated decode, 16 Q / 2 KV "
+                               "heads, head_dim 256, 32768 positions, f16 K/V, "
+                               "f32 q, element-wise gate",
+                   "kv_bytes": kv_bytes, "hbm_peak_fraction": round(
+                       value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles("split_kernel_cfg4"),
+                     "kernel": "split_kernel<f16, 256>",
+                     "kernel_us": round(split_us, 3),
+                     "merge_us": round(ms_merge / max(1, n_merge) * 1e3, 3)},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_decode_baseline(w)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

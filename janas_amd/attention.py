@@ -188,10 +188,12 @@ class Attention:
                              ptr(vs), n, pos0, ptr(out))
         self._last = None
 
-    def run_dev(self, kv_type, seqs, gate_mode=GATE_NONE, stream=None,
+    def prepare(self, kv_type, seqs, gate_mode=GATE_NONE, stream=None,
                 path="auto"):
-        """seqs: a list of dicts with k, v, ks, vs, q, out, gate, last (device
-        arrays or addresses), cap, n, pos0, last_max."""
+        """The call janas_attn_run_dev would make, with its arguments built
+        once: returns a function of no arguments that makes it (the arrays
+        must stay alive). seqs: dicts with k, v, ks, vs, q, out, gate, last
+        (device arrays or addresses), cap, n, pos0, last_max."""
         arr = (Seq * len(seqs))()
         for i, s in enumerate(seqs):
             arr[i] = Seq(ptr(s["k"]), ptr(s["v"]), ptr(s.get("ks")),
@@ -201,9 +203,19 @@ class Attention:
         fn = {"auto": lib().janas_attn_run_dev,
               "split": lib().janas_attn_run_dev_split,
               "prefill": lib().janas_attn_run_dev_prefill}[path]
-        rc = fn(self._a, kv_type, gate_mode, arr, len(seqs), ptr(stream))
-        if rc != 0:
-            raise AttnError(rc, f"janas_attn_run_dev ({path})")
+        a, n, st = self._a, len(seqs), ptr(stream)
+
+        def call():
+            rc = fn(a, kv_type, gate_mode, arr, n, st)
+            if rc != 0:
+                raise AttnError(rc, f"janas_attn_run_dev ({path})")
+        call.keep = (arr, seqs)
+        return call
+
+    def run_dev(self, kv_type, seqs, gate_mode=GATE_NONE, stream=None,
+                path="auto"):
+        """janas_attn_run_dev over a list of sequences (see prepare)."""
+        self.prepare(kv_type, seqs, gate_mode, stream, path)()
 
     def prof_enable(self, on=True):
         lib().janas_attn_prof_enable(self._a, 1 if on else 0)

@@ -13,10 +13,13 @@
  *   split kernel   one workgroup (4 waves of 64) per (sequence, KV head,
  *                  chunk, tile of 16 query rows); a query row is a (token,
  *                  query head of the KV head's group), so every K/V row of
- *                  the chunk is read once for the whole GQA group. Wave w
- *                  takes positions 64w .. 64w + 63 of the chunk.
- *   merge kernel   one wave per (token, query head, 64 columns): the ordered
- *                  merge of the chunk partials, the output gate
+ *                  the chunk is read once for the whole GQA group. The chunk
+ *                  streams through LDS in 4 stages of 64 positions, two
+ *                  buffers deep (the next stage's loads fly while this one
+ *                  is computed); the softmax runs online over the stages and
+ *                  ends in the chunk's exact partial.
+ *   merge kernel   one workgroup per (token, query head, 64 columns): the
+ *                  ordered merge of the chunk partials, the output gate
  *                  sigmoid(g) * o (model_attn.c:159-170) fused in.
  *
  * Scores and values run on the matrix cores (v_mfma_f32_16x16x32_f16) at
@@ -27,12 +30,13 @@
  * one plane; int16: 256 * (x >> 8) and x & 255; f32: hi + lo). Products are
  * exact in the MFMA and summed in f32.
  *
- *   S^T = K . Q^T   A = K rows straight from HBM (16 bytes a lane), B = the
- *                   query planes from LDS; lane l ends with the scores of
- *                   query row l % 16 at positions 4 (l / 16) + i of each
- *                   16-position tile, which is already the A layout P needs.
- *   O   = P . V     A = the weights in registers, B = V rows staged in LDS
- *                   and read back transposed with ds_read_b64_tr_b16.
+ *   S^T = K . Q^T   a stage of 64 positions: wave w scores positions
+ *                   16 w .. 16 w + 15 (A = K rows from LDS, B = the query
+ *                   planes in registers); lane l holds row l % 16 at
+ *                   positions 4 (l / 16) + i.
+ *   O   = P . V     the weights of all 64 positions go through LDS as A
+ *                   operands; wave w sums its quarter of the value columns,
+ *                   V read back transposed with ds_read_b64_tr_b16.
  */
 #include <math.h>
 #include <stdint.h>
@@ -49,11 +53,11 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef short s4 __attribute__((ext_vector_type(4)));
+/* 16 bytes as a native vector (HIP's uint4 is a struct, which keeps large
+   arrays of it out of registers) */
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;
-constexpr int kWavePos = 64;  /* positions a wave */
 constexpr int kRows = 16;     /* query rows a workgroup */
-constexpr int kPad = 16;      /* halves of padding an LDS row */
 
 __device__ __forceinline__ f4 mfma(h8 a, h8 b, f4 c)
 {
@@ -75,11 +79,6 @@ __device__ __forceinline__ h4 lds_read_tr(const _Float16 *p)
     return __builtin_bit_cast(h4, v);
 }
 
-__device__ __forceinline__ h8 cat(h4 a, h4 b)
-{
-    return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
-
 /* x = hi + lo, both f16; x already scaled into f16's normal range */
 __device__ __forceinline__ void split_hl(float x, _Float16 &hi, _Float16 &lo)
 {
@@ -90,9 +89,8 @@ __device__ __forceinline__ void split_hl(float x, _Float16 &hi, _Float16 &lo)
 /* ---- element types of the cache -------------------------------------- */
 
 /*
- * Elem<T>: how 8 consecutive numbers of a K row become the A operand of
- * the score product (load8 / planes8), and how a 16-byte unit of a V row
- * becomes f16 planes in LDS (unit_planes).
+ * Elem<T>: how 8 consecutive numbers of a cached row become f16 planes
+ * whose sum is the number exactly (planes8).
  */
 template <int T> struct Elem;
 
@@ -106,12 +104,6 @@ template <> struct Elem<kF16> {
     __device__ static void planes8(const Raw &r, h8 *p)
     {
         p[0] = __builtin_bit_cast(h8, r.a);
-    }
-    /* 8 numbers a unit */
-    static constexpr int per_unit = 8;
-    __device__ static void unit_planes(uint4 u, h8 *p)
-    {
-        p[0] = __builtin_bit_cast(h8, u);
     }
 };
 
@@ -136,13 +128,6 @@ template <> struct Elem<kI8> {
     {
         p[0] = widen(r.a.x, r.a.y);
     }
-    /* 16 numbers a unit, two groups of 8 halves */
-    static constexpr int per_unit = 16;
-    __device__ static void unit_planes(uint4 u, h8 *p)
-    {
-        p[0] = widen(u.x, u.y);
-        p[1] = widen(u.z, u.w);
-    }
 };
 
 template <> struct Elem<kI16> {
@@ -164,8 +149,6 @@ template <> struct Elem<kI16> {
         }
     }
     __device__ static void planes8(const Raw &r, h8 *p) { split(r.a, p[0], p[1]); }
-    static constexpr int per_unit = 8;
-    __device__ static void unit_planes(uint4 u, h8 *p) { split(u, p[0], p[1]); }
 };
 
 template <> struct Elem<kF32> {
@@ -181,19 +164,6 @@ template <> struct Elem<kF32> {
         uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            _Float16 hi, lo;
-            split_hl(__builtin_bit_cast(float, w[e]), hi, lo);
-            p[0][e] = hi;
-            p[1][e] = lo;
-        }
-    }
-    /* 4 numbers a unit: the first half of each plane's h8 */
-    static constexpr int per_unit = 4;
-    __device__ static void unit_planes(uint4 u, h8 *p)
-    {
-        uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
             _Float16 hi, lo;
             split_hl(__builtin_bit_cast(float, w[e]), hi, lo);
             p[0][e] = hi;
@@ -224,37 +194,65 @@ __device__ __forceinline__ uint32_t row_lo(const SplitArgs &A, uint32_t pos)
     return A.window && pos + 1 > A.window ? pos + 1 - A.window : 0;
 }
 
+/* ---- the split kernel: one shot, every load in flight at once -------- */
+
+/*
+ * A workgroup is 8 waves (2 a SIMD); wave w takes positions 32 w .. 32 w + 31
+ * of the chunk. Every wave issues all its loads at once - the tile's query,
+ * its 32 K rows and its 32 V rows, 16 contiguous bytes a lane (1 KB a wave
+ * instruction, the pattern that streams HBM fastest) - so the chunk's
+ * 256 KB (head_dim 256, f16) are in flight from the first microsecond and
+ * one wave's arithmetic overlaps the others' waiting. K rows pass through a
+ * private LDS region to become the MFMA's A operand; the same region then
+ * holds the V rows, read back transposed. A wave's softmax is one shot over
+ * its 32 positions; the 8 waves' (max, sum, values) are combined at the end.
+ * No load goes straight to LDS: with those in flight the compiler makes
+ * every barrier and every use of a register load wait for all of them.
+ */
+constexpr int kWaves = 8;
+constexpr int kWavePos = kChunk / kWaves; /* 32 */
+constexpr int kBlk = 1024 + 32;           /* LDS bytes of a kilobyte of rows */
+
+/* LDS byte offset of byte b of rows stored a kilobyte at a time, each
+   followed by 32 bytes of padding (spreads the rows over the banks) */
+__device__ __forceinline__ uint32_t blk_off(uint32_t b)
+{
+    return (b >> 10) * kBlk + (b & 1023);
+}
+
 template <int T, int D> struct Shape {
+    static constexpr int EB = Elem<T>::bytes;
     static constexpr int P = Elem<T>::planes;
-    /* value columns staged at a time */
-    static constexpr int VC = P == 1 ? (D < 256 ? D : 256) : (D < 128 ? D : 128);
-    static constexpr int NCB = D / VC;
-    static constexpr int VPITCH = VC + kPad;
-    static constexpr int QPITCH = D + kPad;
-    static constexpr int UPR = D * Elem<T>::bytes / 16;  /* 16-byte units a V row */
-    static constexpr int NT = D / 16;                    /* output column tiles */
-    static constexpr int KS = D / 32;                    /* score k-steps */
-    static constexpr size_t lds_q = 2 * kRows * QPITCH * 2;
-    static constexpr size_t lds_v = (size_t)kWaves * P * 32 * VPITCH * 2;
-    static constexpr size_t lds_acc = (size_t)2 * NT * 64 * 16; /* two buffers */
-    static constexpr size_t lds_va = lds_v > lds_acc ? lds_v : lds_acc;
+    static constexpr bool SCALED = T == kI8 || T == kI16;
+    static constexpr int RB = D * EB;               /* bytes of a (padded) row */
+    static constexpr int WBYTES = kWavePos * RB;    /* a wave's K (or V) rows */
+    static constexpr int UNITS = WBYTES / 1024;     /* 16-byte loads a lane */
+    static constexpr int KS = D / 32;               /* score k-steps */
+    static constexpr int NT = D / 16;               /* output column tiles */
+    static constexpr int QV = D / 128 > 0 ? D / 128 : 1; /* q float4 a lane */
+    static constexpr int QP = D + 16;               /* halves a q row in LDS */
+    /* a wave's region: its rows, later its sums ([NT][64] f4) */
+    static constexpr int RROWS = UNITS * kBlk;
+    static constexpr int RSUM = NT * 64 * 16;
+    static constexpr int REGION = RROWS > RSUM ? RROWS : RSUM;
 };
 
 template <int T, int D>
-__global__ __launch_bounds__(256) void split_kernel(const SplitArgs A)
+__global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
 {
     using E = Elem<T>;
     using S = Shape<T, D>;
     constexpr int P = S::P;
-    __shared__ __attribute__((aligned(16))) _Float16 sQ[2][kRows][S::QPITCH];
-    /* V planes while the values are summed, then the waves' sums */
-    __shared__ __attribute__((aligned(16))) char sVA[S::lds_va];
+    static_assert(S::UNITS >= 1 && S::WBYTES % 1024 == 0, "whole kilobytes a wave");
+    static_assert(2 * S::UNITS + 2 * S::QV + 16 < 63, "the loads fit the wait counter");
+    __shared__ __attribute__((aligned(16))) char sW[kWaves * S::REGION];
+    __shared__ __attribute__((aligned(16))) _Float16 sQ[2][kRows][S::QP];
     __shared__ float sMax[kWaves][kRows], sSum[kWaves][kRows];
-    __shared__ int sExp[kWaves][kRows];
-    __shared__ uint32_t sLo[kRows], sHi[kRows];
     __shared__ float sQs[kRows];
+    __shared__ uint32_t sLo[kRows], sHi[kRows];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t g16 = lane >> 4, l16 = lane & 15;
     const uint32_t id = xcd_remap(blockIdx.x, gridDim.x);
     uint32_t si = 0;
     while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
@@ -270,17 +268,22 @@ __global__ __launch_bounds__(256) void split_kernel(const SplitArgs A)
 
     /* the tile's tokens see [lo(first), last(final)]: nothing of this chunk
        means no partial is needed (the merge does not read it) */
-    {
-        uint32_t jf = r0 / G, jl = (r0 + kRows < R ? r0 + kRows : R) - 1;
-        jl /= G;
-        uint32_t lo = row_lo(A, sq.pos0 + jf);
-        uint32_t hi = sq.last ? sq.last[jl] : sq.pos0 + jl;
-        if (t0 > hi || t0 + kChunk <= lo)
-            return;
-    }
+    const uint32_t rows_here = R - r0 < kRows ? R - r0 : kRows;
+    const uint32_t jf = r0 / G, jl = (r0 + rows_here - 1) / G;
+    const uint32_t lo_all = row_lo(A, sq.pos0 + jf);
+    const uint32_t hi_all = sq.last ? sq.last[jl] : sq.pos0 + jl;
+    if (t0 > hi_all || t0 + kChunk <= lo_all)
+        return;
+    const uint32_t p0w = t0 + w * kWavePos;
+    /* does any row see a position of this wave? (uniform in the wave) */
+    const bool active = p0w <= hi_all && p0w + kWavePos > lo_all;
+    const uint32_t plast = sq.end - 1;
+    /* rows of the chunk in the cache: contiguous, a ring's too (cap is a
+       multiple of the chunk) */
+    const size_t crow = (size_t)kvh * sq.cap + (A.ring ? t0 % sq.cap : t0);
 
-    /* rows: visible range, and the query planes scaled by 2^e so that the
-       largest |q| of the row lies in [2^13, 2^14) */
+    /* rows: visible range (read before the big loads, whose count a wait
+       for last[] would otherwise include) */
     if (tid < kRows) {
         uint32_t r = r0 + tid;
         uint32_t lo = 1, hi = 0;
@@ -292,27 +295,71 @@ __global__ __launch_bounds__(256) void split_kernel(const SplitArgs A)
         sLo[tid] = lo;
         sHi[tid] = hi;
     }
+
+    /* ---- every load, unconditional: rows past the call read its last
+       row, columns past hd column 0 - valid memory whose numbers are masked
+       or multiplied by zero weights ---- */
+    /* q: wave w takes rows 2 w and 2 w + 1, lane l row 2 w + l / 32 */
+    const uint32_t qrow = 2 * w + (lane >> 5);
+    float4 qv[S::QV];
+    bool qok[S::QV];
     {
-        /* 16 threads a row, hd / 16 numbers each (hd a multiple of 8:
-           columns past hd are zero) */
-        const uint32_t qr = tid >> 4, ql = tid & 15, r = r0 + qr;
-        const float *qrow = nullptr;
-        if (r < R) {
-            uint32_t j = r / G, h = kvh * G + r % G;
-            qrow = sq.q + ((size_t)j * A.n_head + h) * hd;
+        const uint32_t r = r0 + qrow < R ? r0 + qrow : r0;
+        const uint32_t j = r / G, h = kvh * G + r % G;
+        const float *src = sq.q + ((size_t)j * A.n_head + h) * hd;
+#pragma unroll
+        for (int i = 0; i < S::QV; i++) {
+            const uint32_t col = 4 * ((lane & 31) + 32 * i);
+            qok[i] = r0 + qrow < R && col < hd && col < D;
+            qv[i] = *(const float4 *)(src + (col < hd ? col : 0));
         }
-        constexpr int PER = D / 16;
-        float v[PER];
+    }
+    /* K and V: byte 1024 i + 16 lane of the wave's 32 rows */
+    u4 kraw[S::UNITS], vraw[S::UNITS];
+    size_t off[S::UNITS];
+#pragma unroll
+    for (int i = 0; i < S::UNITS; i++) {
+        const uint32_t byte = i * 1024 + lane * 16;
+        const uint32_t row = byte / S::RB, cb = byte % S::RB;
+        const uint32_t p = p0w + row;
+        off[i] = (crow + ((p < plast ? p : plast) - t0)) * (hd * S::EB) +
+                 (cb < hd * S::EB ? cb : 0);
+    }
+#pragma unroll
+    for (int i = 0; i < S::UNITS; i++)
+        kraw[i] = *(const u4 *)((const char *)sq.k + off[i]);
+#pragma unroll
+    for (int i = 0; i < S::UNITS; i++)
+        vraw[i] = *(const u4 *)((const char *)sq.v + off[i]);
+    /* the scales of the lane's positions 16 mt + 4 g16 + i */
+    float ks8[8], vs8[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        ks8[e] = 1.0f;
+        vs8[e] = 1.0f;
+    }
+    if constexpr (S::SCALED) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const uint32_t p = p0w + 16 * (e / 4) + 4 * g16 + e % 4;
+            const size_t at = crow + ((p < plast ? p : plast) - t0);
+            ks8[e] = sq.ks[at];
+            vs8[e] = sq.vs[at];
+        }
+    }
+
+    /* ---- q: scaled by 2^e so that the row's largest |q| lies in
+       [2^13, 2^14), split into f16 planes, into LDS ---- */
+    {
         float mx = 0.0f;
 #pragma unroll
-        for (int e = 0; e < PER; e++) {
-            uint32_t col = ql * PER + e;
-            v[e] = qrow && col < hd ? qrow[col] : 0.0f;
-            mx = fmaxf(mx, fabsf(v[e]));
-        }
+        for (int i = 0; i < S::QV; i++)
+            if (qok[i])
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qv[i].x), fabsf(qv[i].y)),
+                                     fmaxf(fabsf(qv[i].z), fabsf(qv[i].w))));
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1)
-            mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        for (int o2 = 1; o2 < 32; o2 <<= 1)
+            mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
         int ex = 0;
         if (mx > 0.0f && mx < INFINITY) {
             frexpf(mx, &ex);
@@ -320,286 +367,244 @@ __global__ __launch_bounds__(256) void split_kernel(const SplitArgs A)
         }
         const float up = ldexpf(1.0f, ex);
 #pragma unroll
-        for (int e = 0; e < PER; e++) {
-            _Float16 hi, lo;
-            split_hl(v[e] * up, hi, lo);
-            sQ[0][qr][ql * PER + e] = hi;
-            sQ[1][qr][ql * PER + e] = lo;
+        for (int i = 0; i < S::QV; i++) {
+            const uint32_t col = 4 * ((lane & 31) + 32 * i);
+            if (col >= D)
+                continue;
+            const float x[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                _Float16 hi, lo;
+                split_hl(qok[i] ? x[e] * up : 0.0f, hi, lo);
+                sQ[0][qrow][col + e] = hi;
+                sQ[1][qrow][col + e] = lo;
+            }
         }
-        if (ql == 0)
-            sQs[qr] = ldexpf(1.0f, -ex);
+        if ((lane & 31) == 0)
+            sQs[qrow] = ldexpf(1.0f, -ex);
     }
     __syncthreads();
 
-    const uint32_t p0w = t0 + w * kWavePos;
-    /* does any row see a position of this wave? */
-    const uint32_t lo_all = sLo[0], hi_all = sHi[(R - r0 < kRows ? R - r0 : kRows) - 1];
-    const bool active = p0w < sq.end && p0w <= hi_all && p0w + kWavePos > lo_all;
-    const size_t head_row = (size_t)kvh * sq.cap;
-    /* rows of the chunk in the cache: contiguous, a ring's too (cap is a
-       multiple of the chunk) */
-    const size_t crow = head_row + (A.ring ? t0 % sq.cap : t0);
-    const uint32_t g16 = lane >> 4, l16 = lane & 15;
-
-    /* ---- loads: the wave's K rows in A layout, its V rows coalesced ---- */
-    typename E::Raw kraw[4][S::KS];
-    uint4 vraw[S::UPR];
+    /* ---- K into the wave's region, then the scores of its two tiles of
+       16 positions (A = K rows 16 mt + l16, B = the query planes) ---- */
+    char *const reg = sW + (size_t)w * S::REGION;
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++) {
-        const uint32_t p = p0w + 16 * mt + l16;
-        const bool ok = active && p < sq.end;
-        const size_t base = (crow + (p - t0)) * hd;
+    for (int i = 0; i < S::UNITS; i++)
+        *(u4 *)(reg + blk_off(i * 1024 + lane * 16)) = kraw[i];
+    f4 sacc[2];
+    {
+        f4 sa[2][2] = {{f4{0, 0, 0, 0}, f4{0, 0, 0, 0}}, {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}}};
 #pragma unroll
-        for (int s = 0; s < S::KS; s++) {
-            const uint32_t d0 = 32 * s + 8 * g16;
-            if (ok && d0 < hd)
-                kraw[mt][s] = E::load8(sq.k, base + d0);
-            else
-                kraw[mt][s] = typename E::Raw{};
-        }
-    }
+        for (int k = 0; k < S::KS; k++) {
+            const h8 qb0 = *(const h8 *)&sQ[0][l16][32 * k + 8 * g16];
+            const h8 qb1 = *(const h8 *)&sQ[1][l16][32 * k + 8 * g16];
 #pragma unroll
-    for (int i = 0; i < S::UPR; i++) {
-        const uint32_t u = i * 64 + lane, row = u / S::UPR, cu = u % S::UPR;
-        const uint32_t p = p0w + row, col = cu * E::per_unit;
-        vraw[i] = uint4{0, 0, 0, 0};
-        if (active && p < sq.end && col < hd) {
-            const char *src = (const char *)sq.v +
-                              ((crow + (p - t0)) * hd + col) * E::bytes;
-            if (col + E::per_unit <= hd) {
-                vraw[i] = *(const uint4 *)src;
-            } else {
-                /* int8 rows of 8 mod 16 numbers: the last unit is half */
-                uint2 h = *(const uint2 *)src;
-                vraw[i].x = h.x;
-                vraw[i].y = h.y;
-            }
-        }
-    }
-
-    /* ---- scores ---- */
-    f4 sacc[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-        sacc[mt] = f4{0, 0, 0, 0};
-    if (active) {
-#pragma unroll
-        for (int s = 0; s < S::KS; s++) {
-            h8 qb[2];
-            qb[0] = *(const h8 *)&sQ[0][l16][32 * s + 8 * g16];
-            qb[1] = *(const h8 *)&sQ[1][l16][32 * s + 8 * g16];
-#pragma unroll
-            for (int mt = 0; mt < 4; mt++) {
+            for (int mt = 0; mt < 2; mt++) {
+                const uint32_t bo = (16 * mt + l16) * S::RB + (32 * k + 8 * g16) * S::EB;
+                typename E::Raw kr;
+                if constexpr (S::EB == 1) {
+                    kr.a = *(const uint2 *)(reg + blk_off(bo));
+                } else if constexpr (S::EB == 2) {
+                    kr.a = *(const uint4 *)(reg + blk_off(bo));
+                } else {
+                    kr.a = *(const uint4 *)(reg + blk_off(bo));
+                    kr.b = *(const uint4 *)(reg + blk_off(bo + 16));
+                }
                 h8 ka[P];
-                E::planes8(kraw[mt][s], ka);
+                E::planes8(kr, ka);
 #pragma unroll
-                for (int kp = 0; kp < P; kp++)
-#pragma unroll
-                    for (int qp = 0; qp < 2; qp++)
-                        if (use_pair<T>(kp, qp))
-                            sacc[mt] = mfma(ka[kp], qb[qp], sacc[mt]);
+                for (int kp = 0; kp < P; kp++) {
+                    if (use_pair<T>(kp, 0))
+                        sa[mt][0] = mfma(ka[kp], qb0, sa[mt][0]);
+                    if (use_pair<T>(kp, 1))
+                        sa[mt][1] = mfma(ka[kp], qb1, sa[mt][1]);
+                }
             }
         }
+        sacc[0] = sa[0][0] + sa[0][1];
+        sacc[1] = sa[1][0] + sa[1][1];
     }
 
-    /* scale, mask; lane l holds row l16 at positions 16 mt + 4 g16 + i */
+    /* ---- the wave's softmax, one shot over its 32 positions: lane l holds
+       row l16 at positions 16 mt + 4 g16 + i ---- */
     const uint32_t rlo = sLo[l16], rhi = sHi[l16];
     const float qs = sQs[l16] * A.scale;
-    const bool scaled = T == kI8 || T == kI16;
-    float sv[4][4];
+    float sv[8];
     float m = -INFINITY;
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t p = p0w + 16 * mt + 4 * g16 + i;
-            float s = -INFINITY;
-            if (active && p >= rlo && p <= rhi && p < sq.end) {
-                s = sacc[mt][i] * qs;
-                if (scaled)
-                    s *= sq.ks[crow + (p - t0)];
-            }
-            sv[mt][i] = s;
-            m = fmaxf(m, s);
+    for (int e = 0; e < 8; e++) {
+        const uint32_t p = p0w + 16 * (e / 4) + 4 * g16 + e % 4;
+        float x = -INFINITY;
+        if (active && p >= rlo && p <= rhi && p <= plast) {
+            x = sacc[e / 4][e % 4] * qs;
+            if constexpr (S::SCALED)
+                x *= ks8[e];
         }
+        sv[e] = x;
+        m = fmaxf(m, x);
+    }
     m = fmaxf(m, __shfl_xor(m, 16, 64));
     m = fmaxf(m, __shfl_xor(m, 32, 64));
-    if (lane < 16)
-        sMax[w][lane] = m;
-    __syncthreads();
-    const float mc = fmaxf(fmaxf(sMax[0][l16], sMax[1][l16]),
-                           fmaxf(sMax[2][l16], sMax[3][l16]));
-
-    /* weights: e^(s - max) of the chunk, 0 when not visible or below
-       e^-80 (attention.c:574-590); their sum; then the value scale */
-    float lsum = 0.0f, pmax = 0.0f;
+    /* the weights' power of two: the largest (e^0 times the largest value
+       scale of the wave's positions) lands in [2^12, 2^13) */
+    int pe = 13;
+    if constexpr (S::SCALED) {
+        float vm = 0.0f;
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+        for (int e = 0; e < 8; e++)
+            vm = fmaxf(vm, vs8[e]);
+        vm = fmaxf(vm, __shfl_xor(vm, 16, 64));
+        vm = fmaxf(vm, __shfl_xor(vm, 32, 64));
+        int ev = 0;
+        if (vm > 0.0f && vm < INFINITY)
+            frexpf(vm, &ev);
+        pe = 13 - ev;
+    }
+    const float up = ldexpf(1.0f, pe);
+    float lsum = 0.0f;
+    /* A operand of the value product: k-slot j is position 4 g16 + j (j < 4)
+       or 16 + 4 g16 + j - 4 - the scores' own layout */
+    h8 pa[2];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float s = sv[mt][i];
-            float pw = 0.0f;
-            if (s != -INFINITY && s - mc >= -80.0f)
-                pw = expf(s - mc);
-            lsum += pw;
-            if (scaled && pw != 0.0f) {
-                const uint32_t p = p0w + 16 * mt + 4 * g16 + i;
-                pw *= sq.vs[crow + (p - t0)];
-            }
-            sv[mt][i] = pw;
-            pmax = fmaxf(pmax, pw);
-        }
+    for (int e = 0; e < 8; e++) {
+        const float x = sv[e];
+        float pw = 0.0f;
+        if (x != -INFINITY && x - m >= -80.0f)
+            pw = expf(x - m);
+        lsum += pw;
+        _Float16 hi, lo;
+        split_hl(pw * vs8[e] * up, hi, lo);
+        pa[0][e] = hi;
+        pa[1][e] = lo;
+    }
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
-    pmax = fmaxf(pmax, __shfl_xor(pmax, 16, 64));
-    pmax = fmaxf(pmax, __shfl_xor(pmax, 32, 64));
-    int pe = 0;
-    if (pmax > 0.0f && pmax < INFINITY) {
-        frexpf(pmax, &pe);
-        pe = 14 - pe;
-    }
-    if (lane < 16) {
-        sSum[w][lane] = lsum;
-        sExp[w][lane] = pe;
-    }
-    /* A operands of the value product: k-slot j of k-step kk is position
-       32 kk + 4 g16 + j (j < 4) or 32 kk + 16 + 4 g16 + j - 4 */
-    h8 pa[2][2];
-    {
-        const float up = ldexpf(1.0f, pe);
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++)
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                _Float16 hi, lo;
-                split_hl(sv[2 * kk + j / 4][j % 4] * up, hi, lo);
-                pa[kk][0][j] = hi;
-                pa[kk][1][j] = lo;
-            }
-    }
 
-    /* ---- values ---- */
+    /* ---- V into the same region (the wave's reads of K are done: LDS
+       serves a wave in order), then the values ---- */
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < S::UNITS; i++)
+        *(u4 *)(reg + blk_off(i * 1024 + lane * 16)) = vraw[i];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     f4 o[S::NT];
 #pragma unroll
-    for (int nt = 0; nt < S::NT; nt++)
-        o[nt] = f4{0, 0, 0, 0};
-    _Float16 *vw = (_Float16 *)sVA + (size_t)w * P * 32 * S::VPITCH;
-    if (active) {
+    for (int t = 0; t < S::NT; t++)
+        o[t] = f4{0, 0, 0, 0};
+    {
+        h8 vbp[S::NT][P];
 #pragma unroll
-        for (int kk = 0; kk < 2; kk++)
+        for (int t = 0; t < S::NT; t++) {
+            if constexpr (S::EB == 2) {
+                const uint32_t r1 = 4 * g16 + (l16 >> 2);
+                const uint32_t cc = 16 * t + 4 * (l16 & 3);
+                const h4 x = lds_read_tr((const _Float16 *)(reg + blk_off(r1 * S::RB + cc * 2)));
+                const h4 y = lds_read_tr((const _Float16 *)(reg + blk_off((r1 + 16) * S::RB + cc * 2)));
+                const h8 xy = h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+                if constexpr (T == kF16)
+                    vbp[t][0] = xy;
+                else
+                    Elem<kI16>::split(__builtin_bit_cast(uint4, xy), vbp[t][0], vbp[t][1]);
+            } else {
+                /* int8 and f32: the 8 positions of one column, one by one */
+                const uint32_t cc = 16 * t + l16;
 #pragma unroll
-            for (int cb = 0; cb < S::NCB; cb++) {
-                /* the wave's rows 32 kk .. 32 kk + 31, columns of block cb,
-                   as f16 planes */
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-                for (int i = 0; i < S::UPR; i++) {
-                    const uint32_t row = (i * 64) / S::UPR;
-                    if ((int)(row / 32) != kk)
-                        continue;
-                    const uint32_t u = i * 64 + lane, rr = u / S::UPR - 32 * kk;
-                    const int col = (int)(u % S::UPR) * E::per_unit - cb * S::VC;
-                    if (col < 0 || col >= S::VC)
-                        continue;
-                    h8 pl[2];
-                    E::unit_planes(vraw[i], pl);
-#pragma unroll
-                    for (int pp = 0; pp < P; pp++) {
-                        _Float16 *dst = vw + ((size_t)pp * 32 + rr) * S::VPITCH + col;
-                        if (T == kF32) {
-                            *(h4 *)dst = h4{pl[pp][0], pl[pp][1], pl[pp][2], pl[pp][3]};
-                        } else if (T == kI8) {
-                            *(h8 *)dst = pl[0];
-                            *(h8 *)(dst + 8) = pl[1];
-                        } else {
-                            *(h8 *)dst = pl[pp];
-                        }
-                    }
-                }
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-                for (int ntl = 0; ntl < S::VC / 16; ntl++) {
-                    const int nt = cb * (S::VC / 16) + ntl;
-                    if (16 * nt >= (int)hd)
-                        continue;
-                    const int tc = 16 * ntl + 4 * (l16 & 3);
-                    const int tr = 4 * g16 + (l16 >> 2);
-#pragma unroll
-                    for (int pp = 0; pp < P; pp++) {
-                        const _Float16 *src = vw + (size_t)pp * 32 * S::VPITCH;
-                        h8 vb = cat(lds_read_tr(src + tr * S::VPITCH + tc),
-                                    lds_read_tr(src + (16 + tr) * S::VPITCH + tc));
-#pragma unroll
-                        for (int ap = 0; ap < 2; ap++)
-                            if (use_pair<T>(pp, ap))
-                                o[nt] = mfma(pa[kk][ap], vb, o[nt]);
+                for (int e = 0; e < 8; e++) {
+                    const uint32_t rv = 16 * (e / 4) + 4 * g16 + e % 4;
+                    const uint32_t bo = blk_off(rv * S::RB + cc * S::EB);
+                    if constexpr (T == kI8) {
+                        vbp[t][0][e] = (_Float16)(int)*(const int8_t *)(reg + bo);
+                    } else {
+                        _Float16 hi, lo;
+                        split_hl(*(const float *)(reg + bo), hi, lo);
+                        vbp[t][0][e] = hi;
+                        vbp[t][1][e] = lo;
                     }
                 }
             }
+        }
+        /* columns past hd hold column 0's numbers: their sums are dropped */
+#pragma unroll
+        for (int ap = 0; ap < 2; ap++)
+#pragma unroll
+            for (int pp = 0; pp < P; pp++)
+                if (use_pair<T>(pp, ap))
+#pragma unroll
+                    for (int t = 0; t < S::NT; t++)
+                        o[t] = mfma(pa[ap], vbp[t][pp], o[t]);
     }
 
-    /* ---- the waves' sums, (w0 + w1) + (w2 + w3), back to 2^0 ---- */
-    float down[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        down[i] = ldexpf(1.0f, -sExp[w][4 * g16 + i]);
-#pragma unroll
-    for (int nt = 0; nt < S::NT; nt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            o[nt][i] *= down[i];
-    __syncthreads();
-    f4 *sacc4 = (f4 *)sVA; /* two buffers of [NT][64] */
-    if (w == 1 || w == 3) {
-        f4 *dst = sacc4 + (size_t)(w / 2) * S::NT * 64;
-#pragma unroll
-        for (int nt = 0; nt < S::NT; nt++)
-            dst[nt * 64 + lane] = o[nt];
+    /* ---- the 8 waves combined: chunk max M, wave w's sums weighted by
+       e^(m_w - M) (and back to 2^0), then wave w adds up its column tiles
+       over the waves in a fixed order and writes them ---- */
+    if (lane < 16) {
+        sMax[w][lane] = m;
+        sSum[w][lane] = lsum;
     }
     __syncthreads();
-    if (w == 0 || w == 2) {
-        const f4 *src = sacc4 + (size_t)(w / 2) * S::NT * 64;
+    float mc = -INFINITY;
 #pragma unroll
-        for (int nt = 0; nt < S::NT; nt++)
-            o[nt] += src[nt * 64 + lane];
-    }
-    __syncthreads();
-    if (w == 2) {
-#pragma unroll
-        for (int nt = 0; nt < S::NT; nt++)
-            sacc4[nt * 64 + lane] = o[nt];
-    }
-    __syncthreads();
-    if (w != 0)
-        return;
-#pragma unroll
-    for (int nt = 0; nt < S::NT; nt++)
-        o[nt] += sacc4[nt * 64 + lane];
-
-    /* ---- the partial of each row that sees the chunk ---- */
-    const uint64_t prow = sq.part0 + ((uint64_t)kvh * sq.span + (c - sq.c0)) * R + r0;
-    if (lane < kRows && r0 + lane < R) {
-        const float l = (sSum[0][lane] + sSum[1][lane]) + (sSum[2][lane] + sSum[3][lane]);
-        const float mx = fmaxf(fmaxf(sMax[0][lane], sMax[1][lane]),
-                               fmaxf(sMax[2][lane], sMax[3][lane]));
-        A.part_ml[(prow + lane) * 2] = mx;
-        A.part_ml[(prow + lane) * 2 + 1] = l;
-    }
-#pragma unroll
-    for (int nt = 0; nt < S::NT; nt++)
+    for (int ww = 0; ww < kWaves; ww++)
+        mc = fmaxf(mc, sMax[ww][l16]);
+    {
+        const float f = (m == -INFINITY ? 0.0f : expf(m - mc)) * ldexpf(1.0f, -pe);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t row = 4 * g16 + i, col = 16 * nt + l16;
-            if (r0 + row < R && col < hd)
-                A.part_acc[(prow + row) * hd + col] = o[nt][i];
+            const float fi = __shfl(f, 4 * g16 + i, 64);
+#pragma unroll
+            for (int t = 0; t < S::NT; t++)
+                o[t][i] *= fi;
         }
+    }
+    /* the region's V reads are done (in order); sums as [NT][64] f4 */
+    f4 *mine = (f4 *)reg;
+#pragma unroll
+    for (int t = 0; t < S::NT; t++)
+        mine[t * 64 + lane] = o[t];
+    __syncthreads();
+    const uint64_t prow = sq.part0 + ((uint64_t)kvh * sq.span + (c - sq.c0)) * R + r0;
+    for (uint32_t t = w; t < (uint32_t)S::NT; t += kWaves) {
+        f4 part[kWaves];
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ww++)
+            part[ww] = ((const f4 *)(sW + (size_t)ww * S::REGION))[t * 64 + lane];
+        const f4 sum = ((part[0] + part[1]) + (part[2] + part[3])) +
+                       ((part[4] + part[5]) + (part[6] + part[7]));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t row = 4 * g16 + i, col = 16 * t + l16;
+            if (r0 + row < R && col < hd)
+                A.part_acc[(prow + row) * hd + col] = sum[i];
+        }
+    }
+    if (w == 0 && lane < kRows && r0 + lane < R) {
+        float l = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ww++) {
+            const float mw = sMax[ww][lane];
+            l += (mw == -INFINITY ? 0.0f : expf(mw - mc)) * sSum[ww][lane];
+        }
+        A.part_ml[(prow + lane) * 2] = mc;
+        A.part_ml[(prow + lane) * 2 + 1] = l;
+    }
 }
 
-/* merge of the chunks of (token j, query head h), 64 columns a wave, in
-   chunk order (attention.c:870-910); then the gate */
-__global__ __launch_bounds__(64) void merge_kernel(const SplitArgs A)
+/*
+ * Merge of the chunk partials of (token j, query head h), 64 columns a
+ * workgroup (attention.c:870-910): the largest chunk score M over all
+ * threads, then group g of 4 sums chunks g, g + 4, ... in order, weights
+ * e^(m_c - M), and the groups are added as (g0 + g1) + (g2 + g3). The order
+ * depends only on the token's own chunk range, so a token merges the same
+ * way in any block. The gate sigmoid(g) * o is applied on the way out.
+ */
+constexpr int kMergeBatch = 16;
+
+__global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 {
-    const uint32_t id = blockIdx.x, lane = threadIdx.x;
+    __shared__ float sRed[4];
+    __shared__ float sAcc[4][64], sL[4];
+    const uint32_t id = blockIdx.x, tid = threadIdx.x, lane = tid & 63,
+                   g = tid >> 6;
     uint32_t si = 0;
     while (si + 1 < A.n_seqs && A.seq[si + 1].mg0 <= id)
         si++;
@@ -610,23 +615,50 @@ __global__ __launch_bounds__(64) void merge_kernel(const SplitArgs A)
     const uint32_t kvh = h / G, r = j * G + h % G, R = sq.n * G;
     const uint32_t pos = sq.pos0 + j;
     const uint32_t lo = row_lo(A, pos), hi = sq.last ? sq.last[j] : pos;
-    const uint32_t clo = lo / kChunk, chi = hi / kChunk;
-    const uint64_t base = sq.part0 + (uint64_t)kvh * sq.span * R + r;
+    const uint32_t clo = lo / kChunk, nc = hi / kChunk - clo + 1;
+    /* partial row of chunk clo + i */
+    const uint64_t base = sq.part0 + ((uint64_t)kvh * sq.span + (clo - sq.c0)) * R + r;
     float mx = -INFINITY;
-    for (uint32_t cc = clo; cc <= chi; cc++)
-        mx = fmaxf(mx, A.part_ml[(base + (uint64_t)(cc - sq.c0) * R) * 2]);
+    for (uint32_t i = tid; i < nc; i += 256)
+        mx = fmaxf(mx, A.part_ml[(base + (uint64_t)i * R) * 2]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0)
+        sRed[g] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(sRed[0], sRed[1]), fmaxf(sRed[2], sRed[3]));
     const uint32_t col = db * 64 + lane;
-    float sum = 0.0f, acc = 0.0f;
-    for (uint32_t cc = clo; cc <= chi; cc++) {
-        const uint64_t pr = base + (uint64_t)(cc - sq.c0) * R;
-        const float wgt = expf(A.part_ml[pr * 2] - mx);
-        sum += wgt * A.part_ml[pr * 2 + 1];
-        if (col < hd)
-            acc = fmaf(wgt, A.part_acc[pr * hd + col], acc);
+    const bool colok = col < hd;
+    float acc = 0.0f, lsum = 0.0f;
+    for (uint32_t i0 = g; i0 < nc; i0 += 4 * kMergeBatch) {
+        float m[kMergeBatch], l[kMergeBatch], v[kMergeBatch];
+        /* branch-free: chunks past the range read the last one, unused */
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; b++) {
+            const uint32_t i = i0 + 4 * b < nc ? i0 + 4 * b : nc - 1;
+            const uint64_t pr = base + (uint64_t)i * R;
+            m[b] = A.part_ml[pr * 2];
+            l[b] = A.part_ml[pr * 2 + 1];
+            v[b] = A.part_acc[pr * hd + (colok ? col : 0)];
+        }
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; b++) {
+            /* past the range: weight 0, adds exact zeros */
+            const float wgt = i0 + 4 * b < nc ? expf(m[b] - mx) : 0.0f;
+            lsum += wgt * l[b];
+            acc = fmaf(wgt, v[b], acc);
+        }
     }
-    if (col >= hd)
+    sAcc[g][lane] = acc;
+    if (lane == 0)
+        sL[g] = lsum;
+    __syncthreads();
+    if (g != 0 || !colok)
         return;
-    float o = acc * (1.0f / sum);
+    const float sum = (sL[0] + sL[1]) + (sL[2] + sL[3]);
+    float o = ((sAcc[0][lane] + sAcc[1][lane]) + (sAcc[2][lane] + sAcc[3][lane])) *
+              (1.0f / sum);
     const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
     if (A.gate_mode == kGateElem)
         o *= 1.0f / (1.0f + expf(-sq.gate[oi]));
@@ -638,7 +670,7 @@ __global__ __launch_bounds__(64) void merge_kernel(const SplitArgs A)
 template <int T, int D>
 hipError_t launch_t(const SplitArgs &a, hipStream_t s)
 {
-    hipLaunchKernelGGL((split_kernel<T, D>), dim3(a.n_wg), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((split_kernel<T, D>), dim3(a.n_wg), dim3(512), 0, s, a);
     return hipGetLastError();
 }
 
@@ -649,8 +681,9 @@ hipError_t launch_d(uint32_t hd, const SplitArgs &a, hipStream_t s)
         return launch_t<T, 64>(a, s);
     if (hd <= 128)
         return launch_t<T, 128>(a, s);
-    if (hd <= 256)
-        return launch_t<T, 256>(a, s);
+    if constexpr (T != kF32)
+        if (hd <= 256)
+            return launch_t<T, 256>(a, s);
     return hipErrorInvalidValue;
 }
 
@@ -658,7 +691,9 @@ hipError_t launch_d(uint32_t hd, const SplitArgs &a, hipStream_t s)
 
 int split_supported(int kv, uint32_t hd)
 {
-    return kv >= kI8 && kv <= kF32 && hd >= 8 && hd % 8 == 0 && hd <= 256;
+    /* f32 rows above 128 numbers would not leave two stages in LDS */
+    return kv >= kI8 && kv <= kF32 && hd >= 8 && hd % 8 == 0 &&
+           hd <= (kv == kF32 ? 128u : 256u);
 }
 
 hipError_t launch_split(int kv, const SplitArgs &a, hipStream_t s)
@@ -678,7 +713,7 @@ hipError_t launch_split(int kv, const SplitArgs &a, hipStream_t s)
 
 hipError_t launch_merge(const SplitArgs &a, uint32_t n_wg, hipStream_t s)
 {
-    hipLaunchKernelGGL(merge_kernel, dim3(n_wg), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(merge_kernel, dim3(n_wg), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
