@@ -157,6 +157,14 @@ int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
                                const struct janas_attn_seq *seqs,
                                uint32_t n_seqs, void *stream);
 
+/* For measurement: the split-KV path's kernels one at a time - kernels 1
+   the split kernel alone (partials only), 2 the merge alone (over the
+   partials a previous call left), 3 both (janas_attn_run_dev_split). */
+int janas_attn_run_dev_kernels(struct janas_attn *a, int kv_type,
+                               int gate_mode,
+                               const struct janas_attn_seq *seqs,
+                               uint32_t n_seqs, void *stream, int kernels);
+
 /* A message for a JANAS_ATTN_E* code. */
 const char *janas_attn_strerror(int err);
 

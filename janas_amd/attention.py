@@ -85,6 +85,10 @@ def lib():
         f.argtypes = [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(Seq),
                       _u32, _vp]
         f.restype = ctypes.c_int
+    L.janas_attn_run_dev_kernels.argtypes = [_vp, ctypes.c_int, ctypes.c_int,
+                                             ctypes.POINTER(Seq), _u32, _vp,
+                                             ctypes.c_int]
+    L.janas_attn_run_dev_kernels.restype = ctypes.c_int
     L.janas_attn_strerror.argtypes = [ctypes.c_int]
     L.janas_attn_strerror.restype = ctypes.c_char_p
     L.janas_attn_prof_enable.argtypes = [_vp, ctypes.c_int]
@@ -200,10 +204,18 @@ class Attention:
                          ptr(s.get("vs")), ptr(s["q"]), ptr(s["out"]),
                          ptr(s.get("gate")), ptr(s.get("last")), s["cap"],
                          s["n"], s["pos0"], s.get("last_max", 0))
-        fn = {"auto": lib().janas_attn_run_dev,
-              "split": lib().janas_attn_run_dev_split,
-              "prefill": lib().janas_attn_run_dev_prefill}[path]
         a, n, st = self._a, len(seqs), ptr(stream)
+        if path in ("split-kernel", "merge-kernel"):
+            # one kernel of the split path alone (measurement)
+            kern = 1 if path == "split-kernel" else 2
+            f = lib().janas_attn_run_dev_kernels
+
+            def fn(a_, kv_, g_, arr_, n_, st_):
+                return f(a_, kv_, g_, arr_, n_, st_, kern)
+        else:
+            fn = {"auto": lib().janas_attn_run_dev,
+                  "split": lib().janas_attn_run_dev_split,
+                  "prefill": lib().janas_attn_run_dev_prefill}[path]
 
         def call():
             rc = fn(a, kv_type, gate_mode, arr, n, st)

@@ -191,7 +191,7 @@ int fill_args(const janas_attn *a, SplitArgs &args, int gate_mode)
 }
 
 int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
-              uint32_t n_seqs, hipStream_t stream)
+              uint32_t n_seqs, hipStream_t stream, int kernels = 3)
 {
     if (!split_supported(kv, a->hd))
         return JANAS_ATTN_ENOTSUP;
@@ -200,7 +200,7 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
         SplitArgs args;
         memset(&args, 0, sizeof args);
         uint64_t rows = 0;
-        uint32_t wg = 0, mg = 0, nd = (a->hd + 63) / 64;
+        uint32_t wg = 0, mg = 0, nd = (a->hd + 31) / 32; /* merge: 32 columns a workgroup */
         for (uint32_t i = 0; i < m; i++) {
             SeqDesc &d = args.seq[i];
             int rc = describe(a, kv, seqs[s0 + i], d);
@@ -223,16 +223,20 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
         args.n_seqs = m;
         args.n_wg = wg;
         fill_args(a, args, gate_mode);
-        ProfEv *ev = prof_begin(a, 0, stream);
-        hipError_t e = launch_split(kv, args, stream);
-        prof_end(ev, stream);
-        if (e != hipSuccess)
-            return hip_err(e, "split launch");
-        ev = prof_begin(a, 1, stream);
-        e = launch_merge(args, mg, stream);
-        prof_end(ev, stream);
-        if (e != hipSuccess)
-            return hip_err(e, "merge launch");
+        if (kernels & 1) {
+            ProfEv *ev = prof_begin(a, 0, stream);
+            hipError_t e = launch_split(kv, args, stream);
+            prof_end(ev, stream);
+            if (e != hipSuccess)
+                return hip_err(e, "split launch");
+        }
+        if (kernels & 2) {
+            ProfEv *ev = prof_begin(a, 1, stream);
+            hipError_t e = launch_merge(args, mg, stream);
+            prof_end(ev, stream);
+            if (e != hipSuccess)
+                return hip_err(e, "merge launch");
+        }
     }
     return JANAS_ATTN_OK;
 }
@@ -623,6 +627,21 @@ extern "C" int janas_attn_run_dev(struct janas_attn *a, int kv_type,
                            (uint32_t)longq.size(), st);
     }
     return run_split(a, kv_type, gate_mode, seqs, n_seqs, st);
+}
+
+extern "C" int janas_attn_run_dev_kernels(struct janas_attn *a, int kv_type,
+                                          int gate_mode,
+                                          const struct janas_attn_seq *seqs,
+                                          uint32_t n_seqs, void *stream,
+                                          int kernels)
+{
+    int rc = check_call(a, kv_type, gate_mode, seqs, n_seqs);
+    if (rc)
+        return rc;
+    if (kernels < 1 || kernels > 3)
+        return JANAS_ATTN_EINVAL;
+    return run_split(a, kv_type, gate_mode, seqs, n_seqs,
+                     stream ? (hipStream_t)stream : a->stream, kernels);
 }
 
 extern "C" const char *janas_attn_strerror(int err)

@@ -328,9 +328,6 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
 #pragma unroll
     for (int i = 0; i < S::UNITS; i++)
         kraw[i] = *(const u4 *)((const char *)sq.k + off[i]);
-#pragma unroll
-    for (int i = 0; i < S::UNITS; i++)
-        vraw[i] = *(const u4 *)((const char *)sq.v + off[i]);
     /* the scales of the lane's positions 16 mt + 4 g16 + i */
     float ks8[8], vs8[8];
 #pragma unroll
@@ -384,6 +381,11 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
             sQs[qrow] = ldexpf(1.0f, -ex);
     }
     __syncthreads();
+    /* V after the barrier: a wave reaches it once its loads are issued, and
+       the memory pipeline accepts them only as fast as data returns */
+#pragma unroll
+    for (int i = 0; i < S::UNITS; i++)
+        vraw[i] = *(const u4 *)((const char *)sq.v + off[i]);
 
     /* ---- K into the wave's region, then the scores of its two tiles of
        16 positions (A = K rows 16 mt + l16, B = the query planes) ---- */
@@ -590,26 +592,30 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
 }
 
 /*
- * Merge of the chunk partials of (token j, query head h), 64 columns a
- * workgroup (attention.c:870-910): the largest chunk score M over all
- * threads, then group g of 4 sums chunks g, g + 4, ... in order, weights
- * e^(m_c - M), and the groups are added as (g0 + g1) + (g2 + g3). The order
- * depends only on the token's own chunk range, so a token merges the same
- * way in any block. The gate sigmoid(g) * o is applied on the way out.
+ * Merge of the chunk partials of (token j, query head h), 32 columns a
+ * workgroup (attention.c:870-910). Group g of 8 (32 lanes each, a lane a
+ * column) takes chunks g, g + 8, ... of the token's range, 16 at a time in
+ * one batch of loads: their largest score M_g, then sum_c e^(m_c - M_g) l_c
+ * and acc_c in chunk order. The groups are combined with weights
+ * e^(M_g - M) as ((g0 + g1) + (g2 + g3)) + ((g4 + g5) + (g6 + g7)). The
+ * order depends only on the token's own chunk range, so a token merges the
+ * same way in any block. The gate sigmoid(g) * o is applied on the way out.
  */
+constexpr int kMergeGroups = 8;
+constexpr int kMergeCols = 32;
 constexpr int kMergeBatch = 16;
 
 __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 {
-    __shared__ float sRed[4];
-    __shared__ float sAcc[4][64], sL[4];
-    const uint32_t id = blockIdx.x, tid = threadIdx.x, lane = tid & 63,
-                   g = tid >> 6;
+    __shared__ float sM[kMergeGroups], sL[kMergeGroups];
+    __shared__ float sAcc[kMergeGroups][kMergeCols];
+    const uint32_t id = blockIdx.x, tid = threadIdx.x;
+    const uint32_t g = tid / kMergeCols, cl = tid % kMergeCols;
     uint32_t si = 0;
     while (si + 1 < A.n_seqs && A.seq[si + 1].mg0 <= id)
         si++;
     const SeqDesc &sq = A.seq[si];
-    const uint32_t hd = A.hd, G = A.group, nd = (hd + 63) / 64;
+    const uint32_t hd = A.hd, G = A.group, nd = (hd + kMergeCols - 1) / kMergeCols;
     const uint32_t local = id - sq.mg0, db = local % nd;
     const uint32_t h = (local / nd) % A.n_head, j = local / nd / A.n_head;
     const uint32_t kvh = h / G, r = j * G + h % G, R = sq.n * G;
@@ -618,46 +624,58 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     const uint32_t clo = lo / kChunk, nc = hi / kChunk - clo + 1;
     /* partial row of chunk clo + i */
     const uint64_t base = sq.part0 + ((uint64_t)kvh * sq.span + (clo - sq.c0)) * R + r;
-    float mx = -INFINITY;
-    for (uint32_t i = tid; i < nc; i += 256)
-        mx = fmaxf(mx, A.part_ml[(base + (uint64_t)i * R) * 2]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if (lane == 0)
-        sRed[g] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(sRed[0], sRed[1]), fmaxf(sRed[2], sRed[3]));
-    const uint32_t col = db * 64 + lane;
+    const uint32_t col = db * kMergeCols + cl;
     const bool colok = col < hd;
-    float acc = 0.0f, lsum = 0.0f;
-    for (uint32_t i0 = g; i0 < nc; i0 += 4 * kMergeBatch) {
-        float m[kMergeBatch], l[kMergeBatch], v[kMergeBatch];
-        /* branch-free: chunks past the range read the last one, unused */
+    float mg = -INFINITY, lg = 0.0f, ag = 0.0f;
+    for (uint32_t i0 = g; i0 < nc; i0 += kMergeGroups * kMergeBatch) {
+        float2 ml[kMergeBatch];
+        float v[kMergeBatch];
+        /* branch-free: chunks past the range read the last one, weight 0 */
 #pragma unroll
         for (int b = 0; b < kMergeBatch; b++) {
-            const uint32_t i = i0 + 4 * b < nc ? i0 + 4 * b : nc - 1;
+            const uint32_t i = i0 + kMergeGroups * b < nc ? i0 + kMergeGroups * b : nc - 1;
             const uint64_t pr = base + (uint64_t)i * R;
-            m[b] = A.part_ml[pr * 2];
-            l[b] = A.part_ml[pr * 2 + 1];
+            ml[b] = *(const float2 *)(A.part_ml + pr * 2);
             v[b] = A.part_acc[pr * hd + (colok ? col : 0)];
         }
+        float mb = mg;
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; b++)
+            if (i0 + kMergeGroups * b < nc)
+                mb = fmaxf(mb, ml[b].x);
+        /* the batch's sums, against the group's new largest score */
+        const float f = mg == -INFINITY ? 0.0f : expf(mg - mb);
+        lg *= f;
+        ag *= f;
 #pragma unroll
         for (int b = 0; b < kMergeBatch; b++) {
-            /* past the range: weight 0, adds exact zeros */
-            const float wgt = i0 + 4 * b < nc ? expf(m[b] - mx) : 0.0f;
-            lsum += wgt * l[b];
-            acc = fmaf(wgt, v[b], acc);
+            const float wgt = i0 + kMergeGroups * b < nc ? expf(ml[b].x - mb) : 0.0f;
+            lg += wgt * ml[b].y;
+            ag = fmaf(wgt, v[b], ag);
         }
+        mg = mb;
     }
-    sAcc[g][lane] = acc;
-    if (lane == 0)
-        sL[g] = lsum;
+    if (cl == 0) {
+        sM[g] = mg;
+        sL[g] = lg;
+    }
+    sAcc[g][cl] = ag;
     __syncthreads();
     if (g != 0 || !colok)
         return;
-    const float sum = (sL[0] + sL[1]) + (sL[2] + sL[3]);
-    float o = ((sAcc[0][lane] + sAcc[1][lane]) + (sAcc[2][lane] + sAcc[3][lane])) *
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kMergeGroups; k++)
+        mx = fmaxf(mx, sM[k]);
+    float wl[kMergeGroups], wa[kMergeGroups];
+#pragma unroll
+    for (int k = 0; k < kMergeGroups; k++) {
+        const float wk = sM[k] == -INFINITY ? 0.0f : expf(sM[k] - mx);
+        wl[k] = wk * sL[k];
+        wa[k] = wk * sAcc[k][cl];
+    }
+    const float sum = ((wl[0] + wl[1]) + (wl[2] + wl[3])) + ((wl[4] + wl[5]) + (wl[6] + wl[7]));
+    float o = (((wa[0] + wa[1]) + (wa[2] + wa[3])) + ((wa[4] + wa[5]) + (wa[6] + wa[7]))) *
               (1.0f / sum);
     const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
     if (A.gate_mode == kGateElem)
