@@ -246,7 +246,6 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
 {
     if (!prefill_supported(kv, a->hd))
         return JANAS_ATTN_ENOTSUP;
-    uint32_t bt = prefill_block_tokens(a->group);
     for (uint32_t s0 = 0; s0 < n_seqs; s0 += kMaxSeqs) {
         uint32_t m = std::min(kMaxSeqs, n_seqs - s0);
         PrefillArgs args;
@@ -258,7 +257,7 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
             if (rc)
                 return rc;
             d.wg0 = wg;
-            uint64_t nwg = (uint64_t)a->n_kv * ((d.n + bt - 1) / bt);
+            uint64_t nwg = (uint64_t)a->n_kv * prefill_row_blocks(d.n, a->group);
             if (wg + nwg > 0x7FFFFFFFu)
                 return JANAS_ATTN_ERANGE;
             wg += (uint32_t)nwg;

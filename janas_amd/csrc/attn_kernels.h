@@ -70,8 +70,8 @@ int split_supported(int kv, uint32_t hd);
 /* attn_prefill.hip */
 hipError_t launch_prefill(int kv, const PrefillArgs &a, hipStream_t s);
 int prefill_supported(int kv, uint32_t hd);
-/* query tokens a prefill workgroup takes */
-uint32_t prefill_block_tokens(uint32_t group);
+/* prefill workgroups a KV head of an n-token sequence takes */
+uint32_t prefill_row_blocks(uint32_t n, uint32_t group);
 
 }  // namespace janas
 

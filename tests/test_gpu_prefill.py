@@ -1,0 +1,235 @@
+"""MFMA prefill path on the GPU against the CPU restatement of the
+reference's attention: BASELINE config 2 (1024-token causal prefill), config
+5's chunked prefill (8192 tokens in calls of 512 over the growing cache),
+and the shapes the engine's callers make (model_attn.c:284-294) - ragged
+lengths, GQA groups that do not divide the tile, padded head sizes, sliding
+windows, a ring cache, set_last spans, the fused gate and several sequences
+a call. The prefill path computes the query and the weights in f16, so the
+bar is the f16 one (max abs error 2e-3 on the normalised outputs).
+"""
+import numpy as np
+import pytest
+import torch
+
+import janas_amd
+from attn_helpers import (KV_F16, TOL_F16_ABS, abs_err, cache, config,
+                          oracle_out, threads)
+from cases import normal
+from janas_amd import Attention
+from oracle import orc
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(x, device):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(device)
+
+
+def prefill_launches(a):
+    return a.prof_read()["prefill"][0]
+
+
+def run_prefill(a, seqs, gpu, gate_mode=0, path="prefill"):
+    """seqs: numpy dicts (k, v, q, pos0, n, optional gate / last); returns
+    the outputs as numpy arrays."""
+    dev = []
+    for s in seqs:
+        d = dict(k=to_dev(s["k"], gpu), v=to_dev(s["v"], gpu),
+                 q=to_dev(np.ascontiguousarray(s["q"], np.float32), gpu),
+                 cap=s["k"].shape[1], n=s["n"], pos0=s["pos0"])
+        d["out"] = torch.full(d["q"].shape, float("nan"), device=gpu)
+        if s.get("gate") is not None:
+            d["gate"] = to_dev(s["gate"], gpu)
+        if s.get("last") is not None:
+            d["last"] = to_dev(s["last"].astype(np.uint32).view(np.int32), gpu)
+            d["last_max"] = int(s["last"].max())
+        dev.append(d)
+    a.run_dev(KV_F16, dev, gate_mode=gate_mode, path=path)
+    torch.cuda.synchronize()
+    return [d["out"].cpu().numpy() for d in dev]
+
+
+def oracle(geom, s, gate_mode=0):
+    out = orc.run(np.ascontiguousarray(s["q"], np.float32), s["k"], s["v"],
+                  n_head=geom["n_head"], n_kv=geom["n_kv"], hd=geom["hd"],
+                  pos0=s["pos0"], kv=KV_F16, scale=geom.get("scale"),
+                  window=geom.get("window", 0), ring=geom.get("ring", False),
+                  last=s.get("last"), threads=threads(), block=64)
+    if gate_mode:
+        orc.gate(out, s["gate"], per_head=gate_mode == janas_amd.GATE_HEAD)
+    return out
+
+
+def test_config2_causal_prefill(gpu):
+    cfg = config(2)
+    s = cfg["seqs"][0]
+    with Attention(cfg["n_head"], cfg["n_kv"], cfg["hd"], s["k"].shape[1]) as a:
+        a.prof_enable(True)
+        (out,) = run_prefill(a, [s], gpu, path="auto")
+        assert prefill_launches(a) == 1, "n > 64 must take the prefill path"
+    ref = oracle_out(orc, cfg, s)
+    err = abs_err(out, ref)
+    print(f"config 2: max abs err {err:.2e}")
+    assert err <= TOL_F16_ABS
+
+
+def test_config5_chunked_prefill(gpu):
+    """An 8192-token prompt in calls of 512 over the cache the earlier calls
+    filled: chunks checked against the restatement, and the chunked result
+    equal bit for bit to one whole-prompt call (a token's tiles and masks do
+    not depend on the call it is in)."""
+    h, kvh, hd, L, step = 32, 8, 128, 8192, 512
+    seed = 20261201
+    k = cache(seed + 11, kvh, L, hd, np.float16)
+    v = cache(seed + 12, kvh, L, hd, np.float16)
+    q = normal(seed + 13, L * h * hd).reshape(L, h, hd)
+    kd, vd, qd = to_dev(k, gpu), to_dev(v, gpu), to_dev(q, gpu)
+    chunked = torch.full(qd.shape, float("nan"), device=gpu)
+    whole = torch.full(qd.shape, float("nan"), device=gpu)
+    with Attention(h, kvh, hd, L) as a:
+        a.prof_enable(True)
+        for p0 in range(0, L, step):
+            a.run_dev(KV_F16, [dict(k=kd, v=vd, q=qd[p0:p0 + step],
+                                    out=chunked[p0:p0 + step], cap=L,
+                                    n=step, pos0=p0)])
+        a.run_dev(KV_F16, [dict(k=kd, v=vd, q=qd, out=whole, cap=L, n=L,
+                                pos0=0)])
+        torch.cuda.synchronize()
+        assert prefill_launches(a) == L // step + 1
+    assert torch.equal(chunked.view(torch.int32), whole.view(torch.int32))
+    out = chunked.cpu().numpy()
+    geom = dict(n_head=h, n_kv=kvh, hd=hd)
+    worst = 0.0
+    for c in (0, 1, 8, 15):
+        p0 = c * step
+        ref = oracle(geom, dict(k=k, v=v, q=q[p0:p0 + step], pos0=p0))
+        worst = max(worst, abs_err(out[p0:p0 + step], ref))
+    print(f"config 5 chunked prefill: max abs err {worst:.2e}")
+    assert worst <= TOL_F16_ABS
+
+
+# (n_head, n_kv, hd, cap, n, pos0, window, scale)
+SHAPES = {
+    "g4_hd128_ragged": (8, 2, 128, 512, 200, 37, 0, None),
+    "g3_hd64": (6, 2, 64, 400, 300, 0, 0, None),
+    "g1_hd96_late": (4, 4, 96, 1400, 129, 1000, 0, None),
+    "g8_hd128_window": (8, 1, 128, 1024, 333, 50, 100, None),
+    "g2_hd40_window_long": (4, 2, 40, 2048, 700, 1200, 513, 0.3),
+    "g5_hd120_n65": (10, 2, 120, 300, 65, 200, 0, None),
+    "g16_hd64": (16, 1, 64, 600, 257, 300, 0, None),
+}
+
+
+@pytest.mark.parametrize("name", sorted(SHAPES))
+def test_prefill_shapes(name, gpu):
+    h, kvh, hd, cap, n, pos0, window, scale = SHAPES[name]
+    seed = 7000 + sorted(SHAPES).index(name)
+    s = dict(k=cache(seed, kvh, cap, hd, np.float16),
+             v=cache(seed + 1, kvh, cap, hd, np.float16),
+             q=normal(seed + 2, n * h * hd).reshape(n, h, hd), pos0=pos0, n=n)
+    geom = dict(n_head=h, n_kv=kvh, hd=hd, scale=scale, window=window)
+    with Attention(h, kvh, hd, cap) as a:
+        if scale is not None:
+            a.set_scale(scale)
+        if window:
+            a.set_window(window)
+        (out,) = run_prefill(a, [s], gpu)
+    ref = oracle(geom, s)
+    err = abs_err(out, ref)
+    print(f"{name}: max abs err {err:.2e}")
+    assert np.isfinite(out).all()
+    assert err <= TOL_F16_ABS
+
+
+@pytest.mark.parametrize("gate_mode", [janas_amd.GATE_ELEM,
+                                       janas_amd.GATE_HEAD])
+def test_prefill_gate(gate_mode, gpu):
+    h, kvh, hd, cap, n = 16, 2, 128, 700, 300
+    g_shape = (n, h, hd) if gate_mode == janas_amd.GATE_ELEM else (n, h)
+    s = dict(k=cache(81, kvh, cap, hd, np.float16),
+             v=cache(82, kvh, cap, hd, np.float16),
+             q=normal(83, n * h * hd).reshape(n, h, hd), pos0=100, n=n,
+             gate=normal(84, int(np.prod(g_shape))).reshape(g_shape))
+    geom = dict(n_head=h, n_kv=kvh, hd=hd, scale=1.0 / 16)
+    with Attention(h, kvh, hd, cap) as a:
+        a.set_scale(1.0 / 16)
+        (out,) = run_prefill(a, [s], gpu, gate_mode=gate_mode)
+    err = abs_err(out, oracle(geom, s, gate_mode))
+    print(f"gate {gate_mode}: max abs err {err:.2e}")
+    assert err <= TOL_F16_ABS
+
+
+def test_prefill_set_last_span(gpu):
+    """A picture's tokens attend both ways within their span
+    (attention.h:89-97)."""
+    h, kvh, hd, cap, n, pos0 = 8, 2, 128, 600, 200, 150
+    p = pos0 + np.arange(n)
+    lo, hi = 230, 290
+    last = np.where((p >= lo) & (p < hi), hi - 1, p).astype(np.uint32)
+    s = dict(k=cache(91, kvh, cap, hd, np.float16),
+             v=cache(92, kvh, cap, hd, np.float16),
+             q=normal(93, n * h * hd).reshape(n, h, hd), pos0=pos0, n=n,
+             last=last)
+    geom = dict(n_head=h, n_kv=kvh, hd=hd)
+    with Attention(h, kvh, hd, cap) as a:
+        (out,) = run_prefill(a, [s], gpu)
+    err = abs_err(out, oracle(geom, s))
+    print(f"set_last span: max abs err {err:.2e}")
+    assert err <= TOL_F16_ABS
+
+
+def test_prefill_ring(gpu):
+    """A sliding-window layer on a ring: position p in row p mod cap."""
+    h, kvh, hd, cap, window, n, pos0 = 8, 2, 128, 1024, 256, 200, 3000
+    s = dict(k=cache(101, kvh, cap, hd, np.float16),
+             v=cache(102, kvh, cap, hd, np.float16),
+             q=normal(103, n * h * hd).reshape(n, h, hd), pos0=pos0, n=n)
+    geom = dict(n_head=h, n_kv=kvh, hd=hd, window=window, ring=True)
+    with Attention(h, kvh, hd, cap) as a:
+        a.set_window(window)
+        a.set_ring(True)
+        (out,) = run_prefill(a, [s], gpu)
+    err = abs_err(out, oracle(geom, s))
+    print(f"ring: max abs err {err:.2e}")
+    assert err <= TOL_F16_ABS
+
+
+def test_prefill_several_sequences(gpu):
+    """Sequences of different lengths and offsets in one launch, each its
+    own cache; each equals its own call bit for bit."""
+    h, kvh, hd = 8, 2, 128
+    seqs = []
+    for i, (cap, n, pos0) in enumerate([(400, 100, 0), (900, 257, 640),
+                                        (300, 70, 1), (2000, 512, 1488)]):
+        seqs.append(dict(k=cache(200 + 3 * i, kvh, cap, hd, np.float16),
+                         v=cache(201 + 3 * i, kvh, cap, hd, np.float16),
+                         q=normal(202 + 3 * i, n * h * hd).reshape(n, h, hd),
+                         pos0=pos0, n=n))
+    geom = dict(n_head=h, n_kv=kvh, hd=hd)
+    with Attention(h, kvh, hd, 2000) as a:
+        outs = run_prefill(a, seqs, gpu)
+        for s, out in zip(seqs, outs):
+            (alone,) = run_prefill(a, [s], gpu)
+            assert np.array_equal(out.view(np.int32), alone.view(np.int32))
+            err = abs_err(out, oracle(geom, s))
+            print(f"n {s['n']} pos0 {s['pos0']}: max abs err {err:.2e}")
+            assert err <= TOL_F16_ABS
+
+
+def test_prefill_refuses_what_it_has_no_kernel_for(gpu):
+    """int8 caches and head sizes above 128 have no prefill kernel:
+    janas_attn_run_dev_prefill says ENOTSUP, janas_attn_run_dev takes the
+    split path."""
+    h, kvh, hd, cap, n = 4, 2, 256, 300, 100
+    s = dict(k=cache(301, kvh, cap, hd, np.float16),
+             v=cache(302, kvh, cap, hd, np.float16),
+             q=normal(303, n * h * hd).reshape(n, h, hd), pos0=0, n=n)
+    with Attention(h, kvh, hd, cap) as a:
+        with pytest.raises(janas_amd.AttnError) as e:
+            run_prefill(a, [s], gpu)
+        assert e.value.code == -5
+        a.prof_enable(True)
+        (out,) = run_prefill(a, [s], gpu, path="auto")
+        assert prefill_launches(a) == 0
+    err = abs_err(out, oracle(dict(n_head=h, n_kv=kvh, hd=hd), s))
+    assert err <= TOL_F16_ABS
