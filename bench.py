@@ -1,13 +1,17 @@
 """Benchmark of the KV-cache attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                    [--only decode|prefill|copy]
 
 Headline (BASELINE.json metric): decode attention KV GB/s at 32k context on
 BASELINE config 4 - 16 query / 2 KV heads, head_dim 256, 32,768 positions,
 f16 K/V, f32 query, gate sigmoid(g) fused - and causal prefill TFLOPS at 8k
 (32 / 8 / 128, 8,192 tokens). A step is one attention call over the resident
 cache (the split kernel and the merge). Inputs are synthetic N(0, 1), drawn
-from a fixed seed, resident in HBM before timing starts.
+from a fixed seed, resident in HBM before timing starts. The prefill figure
+rides along in the same line under "prefill": one causal call over an
+8,192-token prompt, its algorithmic flops (4 x head_dim per visible
+(token, head, position)) over the launch time.
 
 Prints one JSON line. ``roofline`` is the split kernel's: its algorithmic
 bytes (every K/V element of the visible positions once) over its average
@@ -50,6 +54,23 @@ def decode_workload():
                 g=normal(rng, (1, h, hd), np.float32))
 
 
+def prefill_workload():
+    """The 8k causal prefill: BASELINE config 2's heads at 8,192 tokens."""
+    h, kvh, hd, L = 32, 8, 128, 8192
+    rng = np.random.default_rng(SEED + 2)
+    return dict(h=h, kvh=kvh, hd=hd, L=L, scale=1.0 / np.sqrt(hd),
+                k=normal(rng, (kvh, L, hd), np.float16),
+                v=normal(rng, (kvh, L, hd), np.float16),
+                q=normal(rng, (L, h, hd), np.float32))
+
+
+def prefill_flops(hd, h, pos0, n):
+    """4 x head_dim flops per (token, head, visible position): the score
+    and the value product, causal."""
+    seen = n * pos0 + n * (n + 1) / 2
+    return 4.0 * hd * h * seen
+
+
 def traffic_from_profiles(kernel):
     """HBM bytes a launch from profiles/<kernel>_traffic.md (the PMC runs'
     summary), or None."""
@@ -82,6 +103,30 @@ def cpu_decode_baseline(w, budget_s=10.0):
             "cores": cores, "kind": "port",
             "sample": f"config 4 decode call (32768 positions), median of "
                       f"{len(times)} calls, {t * 1e3:.1f} ms each"}
+
+
+def cpu_prefill_baseline(w, block=64):
+    """The restatement on the host's cores over the prompt's last block of
+    64 tokens (the costliest call of the engine's 64-token prefill)."""
+    from oracle import orc
+    cores = max(1, min(16, os.cpu_count() or 1))
+    pos0 = w["L"] - block
+    args = dict(n_head=w["h"], n_kv=w["kvh"], hd=w["hd"], pos0=pos0,
+                kv=orc.KV_F16, scale=float(w["scale"]), threads=cores)
+    q = np.ascontiguousarray(w["q"][pos0:])
+    orc.run(q, w["k"], w["v"], **args)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        orc.run(q, w["k"], w["v"], **args)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    fl = prefill_flops(w["hd"], w["h"], pos0, block)
+    return {"value": round(fl / t / 1e12, 4), "unit": "TFLOP/s",
+            "cores": cores, "kind": "port",
+            "sample": f"last 64-token block of the 8192-token prompt "
+                      f"(positions {pos0}..{w['L'] - 1}), median of 3 calls, "
+                      f"{t * 1e3:.1f} ms each"}
 
 
 NCOPY = 6  # 6 caches of 67 MB: more than the 256 MB infinity cache
@@ -137,6 +182,46 @@ def bench_decode(torch, jm, w, steps, warmup):
     return ms, wall, split_ms, merge_ms
 
 
+def bench_prefill(torch, jm, w, steps, warmup):
+    """One causal prefill call of the whole prompt, launches back to back on
+    a stream of its own, HIP events around them on that stream."""
+    dev = torch.device("cuda:0")
+    k = torch.from_numpy(w["k"]).to(dev)
+    v = torch.from_numpy(w["v"]).to(dev)
+    q = torch.from_numpy(w["q"]).to(dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.Stream()
+    assert stream.cuda_stream != 0
+    with jm.Attention(w["h"], w["kvh"], w["hd"], w["L"]) as a:
+        call = a.prepare(jm.KV_F16, [dict(k=k, v=v, q=q, out=out, cap=w["L"],
+                                          n=w["L"], pos0=0)],
+                         stream=stream.cuda_stream, path="prefill")
+        for _ in range(warmup):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(
+            enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def bench_copy(torch, steps):
+    """A plain 64 MiB device copy: the known-size kernel that scales the
+    HBM byte counters (FETCH_SIZE, WRITE_SIZE) of a profile."""
+    dev = torch.device("cuda:0")
+    src = torch.ones(16 << 20, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": src.numel() * 4,
+                      "copy_bytes_written": dst.numel() * 4}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -144,6 +229,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=("decode", "prefill", "copy"),
+                    help="run one leg alone (profiling)")
+    ap.add_argument("--prefill-steps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is "
@@ -155,9 +243,21 @@ def main():
     jm.lib()
     assert torch.cuda.is_available(), "bench.py needs the GPU"
 
+    if args.only == "copy":
+        bench_copy(torch, args.steps)
+        return
+    if args.only == "prefill":
+        wp = prefill_workload()
+        pms = bench_prefill(torch, jm, wp, args.prefill_steps, 3)
+        print(json.dumps({"prefill_ms": pms}), flush=True)
+        return
     w = decode_workload()
     ms, wall, split_ms, merge_ms = bench_decode(torch, jm, w, args.steps,
                                                 args.warmup)
+    if args.only == "decode":
+        print(json.dumps({"decode_ms": ms, "split_ms": split_ms,
+                          "merge_ms": merge_ms}), flush=True)
+        return
     kv_bytes = 2 * w["kvh"] * w["L"] * w["hd"] * 2
     value = kv_bytes / (ms * 1e-3) / 1e9
     split_us = split_ms * 1e3
@@ -188,8 +288,25 @@ def main():
                      "kernel_us": round(split_us, 3),
                      "merge_us": round(merge_ms * 1e3, 3)},
     }
+    wp = prefill_workload()
+    pms = bench_prefill(torch, jm, wp, args.prefill_steps, 3)
+    fl = prefill_flops(wp["hd"], wp["h"], 0, wp["L"])
+    tf = fl / (pms * 1e-3) / 1e12
+    line["prefill"] = {
+        "metric": "causal prefill attn TFLOP/s @8k",
+        "value": round(tf, 2), "unit": "TFLOP/s", "ms": round(pms, 4),
+        "config": {"workload": "causal prefill, 32 Q / 8 KV heads, head_dim "
+                               "128, 8192 tokens, f16 K/V, f32 q",
+                   "flops": fl},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2),
+                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                     "traffic": traffic_from_profiles("prefill_kernel_8k"),
+                     "kernel": "prefill_kernel<128>"},
+    }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_decode_baseline(w)
+        line["prefill"]["cpu_baseline"] = cpu_prefill_baseline(wp)
     print(json.dumps(line), flush=True)
 
 
