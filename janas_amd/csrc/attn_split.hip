@@ -10,17 +10,24 @@
  * token's result does not depend on the block it runs in, and maps it onto
  * the GPU:
  *
- *   split kernel   one workgroup (4 waves of 64) per (sequence, KV head,
+ *   split kernel   one workgroup (8 waves of 64) per (sequence, KV head,
  *                  chunk, tile of 16 query rows); a query row is a (token,
  *                  query head of the KV head's group), so every K/V row of
- *                  the chunk is read once for the whole GQA group. The chunk
- *                  streams through LDS in 4 stages of 64 positions, two
- *                  buffers deep (the next stage's loads fly while this one
- *                  is computed); the softmax runs online over the stages and
- *                  ends in the chunk's exact partial.
- *   merge kernel   one workgroup per (token, query head, 64 columns): the
- *                  ordered merge of the chunk partials, the output gate
- *                  sigmoid(g) * o (model_attn.c:159-170) fused in.
+ *                  the chunk is read once for the whole GQA group. The whole
+ *                  chunk is in flight at once: wave w loads positions
+ *                  32 w .. 32 w + 31 of K and V with contiguous 16-byte loads
+ *                  (V after the query barrier, so the query's loads are not
+ *                  queued behind it), stages them through its own LDS region
+ *                  into MFMA operand order, and computes a one-shot softmax
+ *                  over its 32 positions; the 8 waves' partials are combined
+ *                  in LDS in a fixed order into the chunk's exact partial.
+ *                  Workgroups are renumbered so each XCD takes a contiguous
+ *                  range (neighbouring chunks share an L2).
+ *   merge kernel   one workgroup per (token, query head, 32 columns): the
+ *                  ordered merge of the chunk partials (8 groups of chunks in
+ *                  parallel, each in batches of 16, combined in a fixed
+ *                  tree), the output gate sigmoid(g) * o (model_attn.c:
+ *                  159-170) fused in.
  *
  * Scores and values run on the matrix cores (v_mfma_f32_16x16x32_f16) at
  * float accuracy: the query and the weights are split into a high and a low
@@ -28,15 +35,17 @@
  * first so that neither part loses bits to f16's range; keys and values
  * enter as f16 planes whose sum is the cached number exactly (int8 and f16:
  * one plane; int16: 256 * (x >> 8) and x & 255; f32: hi + lo). Products are
- * exact in the MFMA and summed in f32.
+ * exact in the MFMA and summed in f32; for an f32 cache the product of the
+ * two low parts (below 2^-22 of a term) is left out.
  *
- *   S^T = K . Q^T   a stage of 64 positions: wave w scores positions
- *                   16 w .. 16 w + 15 (A = K rows from LDS, B = the query
- *                   planes in registers); lane l holds row l % 16 at
- *                   positions 4 (l / 16) + i.
- *   O   = P . V     the weights of all 64 positions go through LDS as A
- *                   operands; wave w sums its quarter of the value columns,
- *                   V read back transposed with ds_read_b64_tr_b16.
+ *   S^T = K . Q^T   wave w scores its 32 positions as two 16-position
+ *                   tiles (A = K rows from LDS, B = the query planes from
+ *                   LDS); lane l holds row l % 16 at positions 4 (l / 16) + i
+ *                   of each tile - already the A layout of the value product.
+ *   O   = P . V     the weights stay in registers as A operands; V is read
+ *                   back transposed with ds_read_b64_tr_b16 (16-bit types)
+ *                   or gathered (int8, f32 planes); every wave sums all
+ *                   value columns over its positions.
  */
 #include <math.h>
 #include <stdint.h>
