@@ -45,7 +45,8 @@ namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef float f4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f16x __attribute__((ext_vector_type(16)));
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
@@ -54,10 +55,16 @@ constexpr int kPRows = 32;                 /* query rows a wave */
 constexpr int kPBlock = kPWaves * kPRows;  /* query rows a workgroup */
 constexpr int kTile = 64;                  /* key positions a tile */
 constexpr float kLog2e = 1.4426950408889634f;
+/* a row's weights are exp2(s - m) against a maximum m that is only moved
+   when a score passes it by more than this (so weights stay below 2^8,
+   well inside f16) - most tiles then need no rescaling */
+constexpr float kSlack = 8.0f;
 
-__device__ __forceinline__ f4 mfma(h8 a, h8 b, f4 c)
+/* v_mfma_f32_32x32x16_f16: lane l holds A[l % 32][8 (l / 32) .. + 7],
+   B[8 (l / 32) .. + 7][l % 32] and D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32] */
+__device__ __forceinline__ f16x mfma(h8 a, h8 b, f16x c)
 {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 /* ds_read_b64_tr_b16 (see attn_split.hip): lane k of a 16-lane group
@@ -84,14 +91,21 @@ __device__ __forceinline__ uint32_t row_lo(const PrefillArgs &A, uint32_t pos)
 template <int D> struct PShape {
     static constexpr int KP = D + 8;   /* halves a K row in LDS (pitch) */
     static constexpr int VP = D + 16;  /* halves a V row in LDS */
-    static constexpr int KS = D / 32;  /* score k-steps */
-    static constexpr int NT = D / 16;  /* output column tiles */
+    static constexpr int KS = D / 16;  /* score k-steps */
+    static constexpr int CT = D / 32;  /* output column tiles */
     /* a tile's 16-byte units of K (and of V), and a thread's share */
     static constexpr int UNITS = kTile * D * 2 / 16;
     static constexpr int UPT = UNITS / (kPWaves * 64);
     static constexpr int UPR = D * 2 / 16;  /* units a row */
 };
 
+/*
+ * Lane l of wave w owns query row r0 + 32 w + l % 32 (half its scores sit
+ * in lane l ^ 32). Scores S^T = K . Q^T: element i of sacc[b] is position
+ * p0 + 32 b + 8 (i / 4) + 4 (l / 32) + i % 4. Outputs O^T = V^T . P^T:
+ * element i of o[c] is column 32 c + 8 (i / 4) + 4 (l / 32) + i % 4 of the
+ * lane's row - so the softmax state and the output of a row share a lane.
+ */
 template <int D>
 __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
 {
@@ -101,7 +115,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
     __shared__ __attribute__((aligned(16))) _Float16 sV[2][kTile][S::VP];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const uint32_t g16 = lane >> 4, l16 = lane & 15;
+    const uint32_t g = lane >> 5, l32 = lane & 31, l16 = lane & 15;
     const uint32_t id = xcd_remap(blockIdx.x, gridDim.x);
     uint32_t si = 0;
     while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
@@ -122,32 +136,29 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
     /* with set_last's bounds any token may see up to the call's end */
     const uint32_t hi_all = sq.last ? sq.end - 1 : sq.pos0 + jl;
     const uint32_t tfirst = lo_all / kTile, tlast = hi_all / kTile;
-    /* the first tile of the ring's or the cache's rows */
     const size_t head_row = (size_t)kvh * sq.cap;
 
-    /* ---- the wave's rows: row-tile rt covers rows 32 w + 16 rt + l16 ---- */
-    uint32_t rlo[2], rhi[2];
-    h8 qb[2][S::KS];
-#pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
-        const uint32_t r = r0 + kPRows * w + 16 * rt + l16;
-        const bool ok = r < R;
-        const uint32_t rr = ok ? r : r0;
-        const uint32_t j = rr / G, h = kvh * G + rr % G;
-        rlo[rt] = ok ? row_lo(A, sq.pos0 + j) : 1;
-        rhi[rt] = ok ? (sq.last ? sq.last[j] : sq.pos0 + j) : 0;
-        const float *qrow = sq.q + ((size_t)j * A.n_head + h) * hd;
+    /* ---- the lane's row ---- */
+    const uint32_t r = r0 + kPRows * w + l32;
+    const bool rok = r < R;
+    const uint32_t rj = (rok ? r : r0) / G;
+    const uint32_t rh = kvh * G + (rok ? r : r0) % G;
+    const uint32_t rlo = rok ? row_lo(A, sq.pos0 + rj) : 1;
+    const uint32_t rhi = rok ? (sq.last ? sq.last[rj] : sq.pos0 + rj) : 0;
+    h8 qb[S::KS];
+    {
+        const float *qrow = sq.q + ((size_t)rj * A.n_head + rh) * hd;
         const float f = A.scale * kLog2e;
 #pragma unroll
         for (int s = 0; s < S::KS; s++) {
-            const uint32_t c = 32 * s + 8 * g16;
-            const bool cok = ok && c < hd;
+            const uint32_t c = 16 * s + 8 * g;
+            const bool cok = rok && c < hd;
             const float4 x0 = *(const float4 *)(qrow + (cok ? c : 0));
             const float4 x1 = *(const float4 *)(qrow + (cok ? c + 4 : 0));
             const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                qb[rt][s][e] = (_Float16)(cok ? xs[e] * f : 0.0f);
+                qb[s][e] = (_Float16)(cok ? xs[e] * f : 0.0f);
         }
     }
 
@@ -178,13 +189,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
         }
     };
 
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
-    f4 o[2][S::NT];
+    /* running state of the lane's row: weights are exp2(s - m) */
+    float m = -INFINITY, lsum = 0.0f;
+    f16x o[S::CT];
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++)
+    for (int c = 0; c < S::CT; c++)
 #pragma unroll
-        for (int t = 0; t < S::NT; t++)
-            o[rt][t] = f4{0, 0, 0, 0};
+        for (int i = 0; i < 16; i++)
+            o[c][i] = 0.0f;
 
     u4 kr[S::UPT], vr[S::UPT];
     load(tfirst, kr, vr);
@@ -192,127 +204,128 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
     __syncthreads();
 
     for (uint32_t tile = tfirst; tile <= tlast; tile++) {
-        const int b = (tile - tfirst) & 1;
+        const int buf = (tile - tfirst) & 1;
         if (tile < tlast)
             load(tile + 1, kr, vr);
         const uint32_t p0 = tile * kTile;
-        /* does any of this wave's rows see only part of the tile, or
-           none of it? (then every score is checked) */
-        bool partial = false;
-#pragma unroll
-        for (int rt = 0; rt < 2; rt++)
-            partial |= !(rlo[rt] <= p0 && rhi[rt] >= p0 + kTile - 1);
-        const bool check = __any(partial);
 
-        /* scores: 4 position tiles x 2 row tiles */
-        f4 sacc[4][2];
+        /* scores less the row's maximum so far (the accumulators start at
+           -m): 2 blocks of 32 positions */
+        const float mref = m == -INFINITY ? 0.0f : m;
+        f16x sacc[2];
 #pragma unroll
-        for (int pt = 0; pt < 4; pt++) {
-            sacc[pt][0] = f4{0, 0, 0, 0};
-            sacc[pt][1] = f4{0, 0, 0, 0};
-        }
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                sacc[b][i] = -mref;
 #pragma unroll
         for (int s = 0; s < S::KS; s++)
 #pragma unroll
-            for (int pt = 0; pt < 4; pt++) {
-                const h8 ka = *(const h8 *)&sK[b][16 * pt + l16][32 * s + 8 * g16];
-                sacc[pt][0] = mfma(ka, qb[0][s], sacc[pt][0]);
-                sacc[pt][1] = mfma(ka, qb[1][s], sacc[pt][1]);
+            for (int b = 0; b < 2; b++) {
+                const h8 ka = *(const h8 *)&sK[buf][32 * b + l32][16 * s + 8 * g];
+                sacc[b] = mfma(ka, qb[s], sacc[b]);
             }
 
-        /* online softmax per row; lane l: row l16 of each row tile at
-           positions 16 pt + 4 g16 + i */
-        h8 pa[2][2];
+        /* masks, only where a row of the wave sees part of the tile */
+        const bool partial = !(rlo <= p0 && rhi >= p0 + kTile - 1);
+        if (__any(partial)) {
 #pragma unroll
-        for (int rt = 0; rt < 2; rt++) {
-            float sv[16];
-            float mt = -INFINITY;
+            for (int b = 0; b < 2; b++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                float x = sacc[e / 4][rt][e % 4];
-                if (check) {
-                    const uint32_t p = p0 + 16 * (e / 4) + 4 * g16 + e % 4;
-                    if (p < rlo[rt] || p > rhi[rt])
-                        x = -INFINITY;
+                for (int i = 0; i < 16; i++) {
+                    const uint32_t p = p0 + 32 * b + 8 * (i / 4) + 4 * g + i % 4;
+                    if (p < rlo || p > rhi)
+                        sacc[b][i] = -INFINITY;
                 }
-                sv[e] = x;
-                mt = fmaxf(mt, x);
-            }
-            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-            const float mn = fmaxf(m[rt], mt);
-            /* a row that has seen nothing yet keeps its zeros */
-            const float ms = mn == -INFINITY ? 0.0f : mn;
-            const float alpha = exp2f(m[rt] - ms);
-            float ls = 0.0f;
+        }
+        float mx = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const float pw = exp2f(sv[e] - ms);
-                ls += pw;
-                pa[rt][e / 8][e % 8] = (_Float16)pw;
-            }
-            l[rt] = l[rt] * alpha + ls;
-            m[rt] = mn;
-            /* rescale the sums: rows 4 g16 + i of the row tile */
+        for (int b = 0; b < 2; b++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float ai = __shfl(alpha, 4 * g16 + i, 64);
+            for (int i = 0; i < 16; i++)
+                mx = fmaxf(mx, sacc[b][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        /* move m when the row has none yet, or a score passed it by more
+           than the slack */
+        const bool move = m == -INFINITY ? mx != -INFINITY : mx > kSlack;
+        if (__any(move)) {
+            const float sh = move ? mx : 0.0f;
+            const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-sh);
+            m = move ? mref + mx : m;
+            lsum *= alpha;
 #pragma unroll
-                for (int t = 0; t < S::NT; t++)
-                    o[rt][t][i] *= ai;
-            }
+            for (int b = 0; b < 2; b++)
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    sacc[b][i] -= sh;
+#pragma unroll
+            for (int c = 0; c < S::CT; c++)
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    o[c][i] *= alpha;
         }
 
-        /* values: k-slot j of k-step kk is position 32 kk + 4 g16 + j
-           (j < 4) or 32 kk + 16 + 4 g16 + j - 4 */
+        /* weights in f16, the PV operands: k-step ks holds positions
+           32 (ks / 2) + 16 (ks % 2) + 8 (e / 4) + 4 (l / 32) + e % 4 */
+        h8 pa[4];
+        float ls = 0.0f;
 #pragma unroll
-        for (int t = 0; t < S::NT; t++) {
-            const uint32_t tr = 4 * g16 + (l16 >> 2), tc = 16 * t + 4 * (l16 & 3);
+        for (int ks = 0; ks < 4; ks++) {
 #pragma unroll
-            for (int kk = 0; kk < 2; kk++) {
-                const h4 x = lds_read_tr(&sV[b][32 * kk + tr][tc]);
-                const h4 y = lds_read_tr(&sV[b][32 * kk + 16 + tr][tc]);
-                const h8 vb = h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-                o[0][t] = mfma(pa[0][kk], vb, o[0][t]);
-                o[1][t] = mfma(pa[1][kk], vb, o[1][t]);
+            for (int e = 0; e < 8; e++)
+                pa[ks][e] = (_Float16)__builtin_amdgcn_exp2f(sacc[ks / 2][8 * (ks % 2) + e]);
+#pragma unroll
+            for (int e = 0; e < 8; e += 2)
+                ls = __builtin_amdgcn_fdot2(h2{pa[ks][e], pa[ks][e + 1]},
+                                            h2{(_Float16)1.0f, (_Float16)1.0f},
+                                            ls, false);
+        }
+        lsum += ls;
+
+        /* O^T += V^T . P^T */
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const uint32_t tr = 16 * ks + 4 * g + (l16 >> 2);
+#pragma unroll
+            for (int c = 0; c < S::CT; c++) {
+                const uint32_t tc = 32 * c + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
+                const h4 x = lds_read_tr(&sV[buf][tr][tc]);
+                const h4 y = lds_read_tr(&sV[buf][tr + 8][tc]);
+                const h8 va = h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+                o[c] = mfma(va, pa[ks], o[c]);
             }
         }
         if (tile < tlast) {
             __syncthreads(); /* every wave is done with the other buffer */
-            store(b ^ 1, kr, vr);
+            store(buf ^ 1, kr, vr);
             __syncthreads();
         }
     }
 
-    /* ---- out = sums / weights, gated; lane l holds rows 4 g16 + i ---- */
+    /* ---- out = sums / weights, gated ---- */
+    const float lt = lsum + __shfl_xor(lsum, 32, 64);
+    if (!rok)
+        return;
+    const float inv = 1.0f / lt;
+    const size_t obase = ((size_t)rj * A.n_head + rh) * hd;
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
-        float lt = l[rt];
-        lt += __shfl_xor(lt, 16, 64);
-        lt += __shfl_xor(lt, 32, 64);
+    for (int c = 0; c < S::CT; c++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float li = __shfl(lt, 4 * g16 + i, 64);
-            const uint32_t r = r0 + kPRows * w + 16 * rt + 4 * g16 + i;
-            if (r >= R)
+        for (int q4 = 0; q4 < 4; q4++) {
+            const uint32_t col = 32 * c + 8 * q4 + 4 * g;
+            if (col >= hd)
                 continue;
-            const uint32_t j = r / G, h = kvh * G + r % G;
-            const float inv = 1.0f / li;
+            float x[4];
 #pragma unroll
-            for (int t = 0; t < S::NT; t++) {
-                const uint32_t col = 16 * t + l16;
-                if (col >= hd)
-                    continue;
-                const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
-                float x = o[rt][t][i] * inv;
+            for (int e = 0; e < 4; e++) {
+                x[e] = o[c][4 * q4 + e] * inv;
                 if (A.gate_mode == kGateElem)
-                    x *= 1.0f / (1.0f + expf(-sq.gate[oi]));
+                    x[e] *= 1.0f / (1.0f + expf(-sq.gate[obase + col + e]));
                 else if (A.gate_mode == kGateHead)
-                    x *= 1.0f / (1.0f + expf(-sq.gate[(size_t)j * A.n_head + h]));
-                sq.out[oi] = x;
+                    x[e] *= 1.0f / (1.0f + expf(-sq.gate[(size_t)rj * A.n_head + rh]));
             }
+            *(float4 *)(sq.out + obase + col) = float4{x[0], x[1], x[2], x[3]};
         }
-    }
 }
 
 template <int D>
