@@ -131,6 +131,25 @@ struct janas_attn_seq {
     uint32_t n;           /* tokens */
     uint32_t pos0;        /* position of the first */
     uint32_t last_max;    /* with last: last[n - 1]; ignored otherwise */
+    /* or NULL: the output (gated) also as Q8_K blocks for the next product,
+       n x (n_head * head_dim / 256) struct janas_attn_q8k, as att_out_tok
+       makes them (model_attn.c:159-170); n_head * head_dim a multiple of
+       256 */
+    void *out_q8k;
+};
+
+/* struct janas_block_q8k (src/llm/quant.h:283-300): 256 numbers as int8
+   with one scale, their sums of 16, the same numbers in 8 blocks of 32 with
+   scales of their own and their sums, and the sums of 32 - 628 bytes. */
+#define JANAS_ATTN_QK 256
+struct janas_attn_q8k {
+    float d;
+    int8_t qs[JANAS_ATTN_QK];
+    int16_t bsums[JANAS_ATTN_QK / 16];
+    float d32[8];
+    int8_t qs32[JANAS_ATTN_QK];
+    int16_t bsums32[JANAS_ATTN_QK / 16];
+    int16_t bsums2[JANAS_ATTN_QK / 32];
 };
 
 /*
@@ -179,6 +198,75 @@ const char *janas_attn_strerror(int err);
 void janas_attn_prof_enable(struct janas_attn *a, int on);
 int janas_attn_prof_read(struct janas_attn *a, uint32_t counts[3],
                          double ms[3]);
+
+/* ===== Part 3: the cache around the attention ========================
+   The rules the engine applies to a layer's cache besides reading it
+   (src/llm/model_attn.c, model.c, model_state.c), on the device. No
+   counterpart in attention.h: the engine does these on the CPU. All take a
+   stream (NULL: the default stream), are asynchronous, and return 0 or a
+   negative JANAS_ATTN_E* code. */
+
+/* One layer's cache on the device. */
+struct janas_attn_cache {
+    void *k, *v;          /* n_kv x cap x head_dim elements of kv_type */
+    float *ks, *vs;       /* n_kv x cap scales (int8 / int16 caches) */
+    uint32_t n_kv;
+    uint32_t head_dim;    /* up to 512 */
+    uint32_t cap;         /* rows a KV head */
+    int kv_type;          /* enum janas_attn_kv */
+    int ring;             /* position p in row p mod cap */
+};
+
+/*
+ * qkv_item's key and value part (model_attn.c:75-146) for tokens pos0 ..
+ * pos0 + n - 1: each key row of k (n x n_kv x head_dim floats, device) is
+ * rms-normalized with k_norm (head_dim weights, or NULL: none), turned by
+ * the NeoX RoPE of its token (cs, sn: n x n_rot / 2 device floats, the
+ * engine's tables), each value row of v optionally normalized without
+ * weights (v_norm, Gemma 4), and both written into the cache - int8 or
+ * int16 with a scale of their own (the largest magnitude becomes 127 or
+ * 32767), f16 or f32 as they are. k and v are not modified. Bit for bit the
+ * reference's arithmetic.
+ */
+int janas_attn_cache_write(const struct janas_attn_cache *c, const float *k,
+                           const float *v, const float *k_norm, float eps,
+                           const float *cs, const float *sn, uint32_t n_rot,
+                           int v_norm, uint32_t pos0, uint32_t n,
+                           void *stream);
+
+/* The query side of qkv_item (model_attn.c:86-97): rows of q
+   (n x n_head x head_dim, device) normalized with q_norm (or not) and
+   turned, in place. */
+int janas_attn_q_prep(float *q, const float *q_norm, float eps,
+                      const float *cs, const float *sn, uint32_t n_rot,
+                      uint32_t n, uint32_t n_head, uint32_t head_dim,
+                      void *stream);
+
+/*
+ * One layer's part of janas_llm_model_shift (model.c:292-377): of the n_pos
+ * positions, keep .. keep + drop - 1 are forgotten and the ones after them
+ * move down by drop, their keys turned back by the angles of drop positions
+ * (cs, sn: n_rot / 2 device floats, as the engine computes them:
+ * model.c:323-329) and quantized anew; a ring moves the positions it still
+ * holds. int8 / int16 caches. Allocates a copy of the moved rows for the
+ * call (and synchronizes the stream to free it).
+ */
+int janas_attn_cache_shift(const struct janas_attn_cache *c, uint32_t keep,
+                           uint32_t drop, uint32_t n_pos, const float *cs,
+                           const float *sn, uint32_t n_rot, void *stream);
+
+/*
+ * The rows a saved state holds (copy_kv, model_state.c:175-218): of a state
+ * of n_pos positions, `rows` positions of every KV head - 0 .. rows - 1, or
+ * for a ring the last rows (n_pos - rows .. n_pos - 1, wherever the ring
+ * has them) - packed head after head in position order: k, v rows x n_kv x
+ * head_dim elements, ks, vs rows x n_kv floats (int8 / int16; NULL
+ * otherwise). out 1: cache to the buffers; 0: buffers to the cache. The
+ * buffers may be host or device memory.
+ */
+int janas_attn_cache_copy(const struct janas_attn_cache *c, uint32_t n_pos,
+                          uint32_t rows, void *k, void *v, float *ks,
+                          float *vs, int out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -36,7 +36,17 @@ class Seq(ctypes.Structure):
     _fields_ = [("k", _vp), ("v", _vp), ("ks", _vp), ("vs", _vp),
                 ("q", _vp), ("out", _vp), ("gate", _vp), ("last", _vp),
                 ("cap", _u32), ("n", _u32), ("pos0", _u32),
-                ("last_max", _u32)]
+                ("last_max", _u32), ("out_q8k", _vp)]
+
+
+class Cache(ctypes.Structure):
+    """struct janas_attn_cache (include/janas_attn.h Part 3)."""
+    _fields_ = [("k", _vp), ("v", _vp), ("ks", _vp), ("vs", _vp),
+                ("n_kv", _u32), ("head_dim", _u32), ("cap", _u32),
+                ("kv_type", ctypes.c_int), ("ring", ctypes.c_int)]
+
+
+Q8K_BYTES = 628  # struct janas_attn_q8k
 
 
 class AttnError(RuntimeError):
@@ -91,6 +101,19 @@ def lib():
     L.janas_attn_run_dev_kernels.restype = ctypes.c_int
     L.janas_attn_strerror.argtypes = [ctypes.c_int]
     L.janas_attn_strerror.restype = ctypes.c_char_p
+    L.janas_attn_cache_write.argtypes = [ctypes.POINTER(Cache), _vp, _vp,
+                                         _vp, ctypes.c_float, _vp, _vp, _u32,
+                                         ctypes.c_int, _u32, _u32, _vp]
+    L.janas_attn_cache_write.restype = ctypes.c_int
+    L.janas_attn_q_prep.argtypes = [_vp, _vp, ctypes.c_float, _vp, _vp, _u32,
+                                    _u32, _u32, _u32, _vp]
+    L.janas_attn_q_prep.restype = ctypes.c_int
+    L.janas_attn_cache_shift.argtypes = [ctypes.POINTER(Cache), _u32, _u32,
+                                         _u32, _vp, _vp, _u32, _vp]
+    L.janas_attn_cache_shift.restype = ctypes.c_int
+    L.janas_attn_cache_copy.argtypes = [ctypes.POINTER(Cache), _u32, _u32,
+                                        _vp, _vp, _vp, _vp, ctypes.c_int, _vp]
+    L.janas_attn_cache_copy.restype = ctypes.c_int
     L.janas_attn_prof_enable.argtypes = [_vp, ctypes.c_int]
     L.janas_attn_prof_read.argtypes = [_vp, ctypes.POINTER(_u32),
                                        ctypes.POINTER(ctypes.c_double)]
@@ -203,7 +226,8 @@ class Attention:
             arr[i] = Seq(ptr(s["k"]), ptr(s["v"]), ptr(s.get("ks")),
                          ptr(s.get("vs")), ptr(s["q"]), ptr(s["out"]),
                          ptr(s.get("gate")), ptr(s.get("last")), s["cap"],
-                         s["n"], s["pos0"], s.get("last_max", 0))
+                         s["n"], s["pos0"], s.get("last_max", 0),
+                         ptr(s.get("out_q8k")))
         a, n, st = self._a, len(seqs), ptr(stream)
         if path in ("split-kernel", "merge-kernel"):
             # one kernel of the split path alone (measurement)
@@ -241,3 +265,52 @@ class Attention:
             raise AttnError(rc, "janas_attn_prof_read")
         return {name: (counts[i], ms[i])
                 for i, name in enumerate(("split", "merge", "prefill"))}
+
+
+# ---- Part 3: the cache around the attention --------------------------------
+
+def _check(rc, what):
+    if rc != 0:
+        raise AttnError(rc, what)
+
+
+def cache(k, v, ks=None, vs=None, *, kv_type, ring=False):
+    """struct janas_attn_cache over device tensors k, v (n_kv, cap, hd) and
+    ks, vs (n_kv, cap)."""
+    n_kv, cap, hd = k.shape
+    return Cache(ptr(k), ptr(v), ptr(ks), ptr(vs), n_kv, hd, cap, kv_type,
+                 1 if ring else 0)
+
+
+def cache_write(c, k, v, *, cs, sn, n_rot, pos0, k_norm=None, eps=1e-6,
+                v_norm=False, stream=None):
+    """janas_attn_cache_write: k, v (n, n_kv, hd) device floats."""
+    _check(lib().janas_attn_cache_write(ctypes.byref(c), ptr(k), ptr(v),
+                                        ptr(k_norm), eps, ptr(cs), ptr(sn),
+                                        n_rot, 1 if v_norm else 0, pos0,
+                                        k.shape[0], ptr(stream)),
+           "janas_attn_cache_write")
+
+
+def q_prep(q, *, cs, sn, n_rot, q_norm=None, eps=1e-6, stream=None):
+    """janas_attn_q_prep on q (n, n_head, hd), in place."""
+    n, n_head, hd = q.shape
+    _check(lib().janas_attn_q_prep(ptr(q), ptr(q_norm), eps, ptr(cs), ptr(sn),
+                                   n_rot, n, n_head, hd, ptr(stream)),
+           "janas_attn_q_prep")
+
+
+def cache_shift(c, *, keep, drop, n_pos, cs, sn, n_rot, stream=None):
+    """janas_attn_cache_shift."""
+    _check(lib().janas_attn_cache_shift(ctypes.byref(c), keep, drop, n_pos,
+                                        ptr(cs), ptr(sn), n_rot, ptr(stream)),
+           "janas_attn_cache_shift")
+
+
+def cache_copy(c, *, n_pos, rows, k, v, ks=None, vs=None, out=True,
+               stream=None):
+    """janas_attn_cache_copy: out=True cache -> buffers, else back."""
+    _check(lib().janas_attn_cache_copy(ctypes.byref(c), n_pos, rows, ptr(k),
+                                       ptr(v), ptr(ks), ptr(vs),
+                                       1 if out else 0, ptr(stream)),
+           "janas_attn_cache_copy")

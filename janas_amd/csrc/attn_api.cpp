@@ -121,6 +121,30 @@ int describe(const janas_attn *a, int kv, const janas_attn_seq &s, SeqDesc &d)
         return JANAS_ATTN_ERANGE;
     }
     d.rtiles = (s.n * a->group + 15) / 16;
+    if (s.out_q8k && ((uint64_t)a->n_head * a->hd) % JANAS_ATTN_QK)
+        return JANAS_ATTN_EINVAL;
+    return JANAS_ATTN_OK;
+}
+
+/* The outputs also as Q8_K blocks where a sequence asks for them
+   (att_out_tok, model_attn.c:159-170: the gate is already in the output). */
+int put_q8k(const janas_attn *a, const janas_attn_seq *seqs, uint32_t n_seqs,
+            hipStream_t stream)
+{
+    for (uint32_t i = 0; i < n_seqs; i++) {
+        if (!seqs[i].out_q8k)
+            continue;
+        Q8kArgs q;
+        q.x = seqs[i].out;
+        q.y = (uint8_t *)seqs[i].out_q8k;
+        uint64_t blocks = (uint64_t)seqs[i].n * a->n_head * a->hd / JANAS_ATTN_QK;
+        if (blocks > 0x7FFFFFFFu)
+            return JANAS_ATTN_ERANGE;
+        q.blocks = (uint32_t)blocks;
+        hipError_t e = launch_q8k(q, stream);
+        if (e != hipSuccess)
+            return hip_err(e, "q8k launch");
+    }
     return JANAS_ATTN_OK;
 }
 
@@ -582,8 +606,9 @@ extern "C" int janas_attn_run_dev_split(struct janas_attn *a, int kv_type,
     int rc = check_call(a, kv_type, gate_mode, seqs, n_seqs);
     if (rc)
         return rc;
-    return run_split(a, kv_type, gate_mode, seqs, n_seqs,
-                     stream ? (hipStream_t)stream : a->stream);
+    hipStream_t st = stream ? (hipStream_t)stream : a->stream;
+    rc = run_split(a, kv_type, gate_mode, seqs, n_seqs, st);
+    return rc ? rc : put_q8k(a, seqs, n_seqs, st);
 }
 
 extern "C" int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
@@ -594,8 +619,9 @@ extern "C" int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
     int rc = check_call(a, kv_type, gate_mode, seqs, n_seqs);
     if (rc)
         return rc;
-    return run_prefill(a, kv_type, gate_mode, seqs, n_seqs,
-                       stream ? (hipStream_t)stream : a->stream);
+    hipStream_t st = stream ? (hipStream_t)stream : a->stream;
+    rc = run_prefill(a, kv_type, gate_mode, seqs, n_seqs, st);
+    return rc ? rc : put_q8k(a, seqs, n_seqs, st);
 }
 
 extern "C" int janas_attn_run_dev(struct janas_attn *a, int kv_type,
@@ -622,10 +648,12 @@ extern "C" int janas_attn_run_dev(struct janas_attn *a, int kv_type,
             if (rc)
                 return rc;
         }
-        return run_prefill(a, kv_type, gate_mode, longq.data(),
-                           (uint32_t)longq.size(), st);
+        rc = run_prefill(a, kv_type, gate_mode, longq.data(),
+                         (uint32_t)longq.size(), st);
+    } else {
+        rc = run_split(a, kv_type, gate_mode, seqs, n_seqs, st);
     }
-    return run_split(a, kv_type, gate_mode, seqs, n_seqs, st);
+    return rc ? rc : put_q8k(a, seqs, n_seqs, st);
 }
 
 extern "C" int janas_attn_run_dev_kernels(struct janas_attn *a, int kv_type,

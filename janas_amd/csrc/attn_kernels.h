@@ -60,12 +60,52 @@ struct PrefillArgs {
     int gate_mode;
 };
 
+/* Rows of a cache write or of the query preparation (attn_cache.hip). */
+struct RowArgs {
+    float *k;              /* n x heads x hd: keys, or the queries (in place) */
+    const float *v;        /* n x heads x hd values, or null (queries) */
+    const float *norm;     /* hd weights of the key (query) norm, or null */
+    const float *cs, *sn;  /* n x n_rot / 2 */
+    void *kc, *vc;         /* the cache, heads x cap x hd; null: queries */
+    float *kz, *vz;        /* heads x cap scales (int8 / int16) */
+    float eps;
+    uint32_t n, heads, hd, n_rot, pos0, cap;
+    int kv, ring, v_norm;
+};
+
+/* Rows a context shift moves (attn_cache.hip). The copy holds copy_rows
+   rows a KV head: rows copy_first .. of the cache, or all of a ring's. */
+struct ShiftArgs {
+    void *k, *v;
+    float *kz, *vz;
+    const void *ck, *cv;   /* the copy */
+    const float *ckz, *cvz;
+    const float *cs, *sn;  /* the shift's angles, n_rot / 2 */
+    uint32_t n_kv, hd, cap, n_rot;
+    uint32_t first, count; /* positions first .. first + count - 1 move */
+    uint32_t drop, copy_first, copy_rows;
+    int kv, ring;
+};
+
+/* Q8_K blocks of output rows (struct janas_block_q8k, 628 bytes). */
+constexpr uint32_t kQ8kBytes = 628;
+struct Q8kArgs {
+    const float *x;        /* blocks x 256 */
+    uint8_t *y;            /* blocks x 628 bytes */
+    uint32_t blocks;
+};
+
 /* Launchers (attn_split.hip). Return hipSuccess or the launch's error. */
 hipError_t launch_split(int kv, const SplitArgs &a, hipStream_t s);
 hipError_t launch_merge(const SplitArgs &a, uint32_t n_wg, hipStream_t s);
 /* 1 when the split kernel has an instance for this element type and
    padded head size. */
 int split_supported(int kv, uint32_t hd);
+
+/* attn_cache.hip */
+hipError_t launch_rows(const RowArgs &a, hipStream_t s);
+hipError_t launch_shift(const ShiftArgs &a, hipStream_t s);
+hipError_t launch_q8k(const Q8kArgs &a, hipStream_t s);
 
 /* attn_prefill.hip */
 hipError_t launch_prefill(int kv, const PrefillArgs &a, hipStream_t s);

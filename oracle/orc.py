@@ -4,7 +4,8 @@ Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
 this module. It wraps two shared libraries built by oracle/Makefile:
 
 * ``liborc_attn.so``: this repo's C restatement of the reference attention
-  (oracle/attn_oracle.c), generic over the cache's element type;
+  (oracle/attn_oracle.c), generic over the cache's element type, and of the
+  cache-side rules - cache write, shift, Q8_K (oracle/cache_oracle.c);
 * ``_ref/libjanas_ref_attn.so``: the reference's own attention compiled from
   /root/reference/src/llm/attention.c and its few dependencies, driven through
   its public header (src/llm/attention.h:58-112). It is used to write the
@@ -59,6 +60,23 @@ def orc():
         lib.orc_f16_to_f32.restype = ctypes.c_float
         lib.orc_ring_positions.argtypes = [_u32, _u32]
         lib.orc_ring_positions.restype = _u32
+        lib.orc_q8k_quantize.argtypes = [_vp, _vp, ctypes.c_size_t]
+        lib.orc_q8k_quantize.restype = None
+        lib.orc_cache_write.argtypes = [_vp, _vp, _vp, ctypes.c_float, _vp,
+                                        _vp, _u32, ctypes.c_int, _u32, _u32,
+                                        _u32, _u32, _u32, ctypes.c_int,
+                                        ctypes.c_int, _vp, _vp, _vp, _vp]
+        lib.orc_cache_write.restype = None
+        lib.orc_q_prep.argtypes = [_vp, _vp, ctypes.c_float, _vp, _vp, _u32,
+                                   _u32, _u32, _u32]
+        lib.orc_q_prep.restype = None
+        lib.orc_unrotate_row.argtypes = [_vp, _vp, _u32, _u32, _vp, _vp,
+                                         ctypes.c_int]
+        lib.orc_unrotate_row.restype = None
+        lib.orc_cache_shift.argtypes = [_vp, _vp, _vp, _vp, _u32, _u32, _u32,
+                                        ctypes.c_int, ctypes.c_int, _u32, _u32,
+                                        _u32, _vp, _vp, _u32]
+        lib.orc_cache_shift.restype = ctypes.c_int
         _orc = lib
     return _orc
 
@@ -137,6 +155,89 @@ def exp_det(x):
 
 def ring_positions(window, n):
     return orc().orc_ring_positions(window, n)
+
+
+# struct janas_block_q8k (src/llm/quant.h:283-300), 628 bytes
+Q8K = np.dtype([("d", "<f4"), ("qs", "i1", 256), ("bsums", "<i2", 16),
+                ("d32", "<f4", 8), ("qs32", "i1", 256),
+                ("bsums32", "<i2", 16), ("bsums2", "<i2", 8)])
+assert Q8K.itemsize == 628
+
+
+def q8k_quantize(x):
+    """x (..., 256 m) float32 -> (..., m) Q8K blocks, the restatement of
+    janas_q8k_quantize (quant.c:174-200)."""
+    x = np.ascontiguousarray(x, np.float32)
+    assert x.shape[-1] % 256 == 0
+    y = np.zeros(x.shape[:-1] + (x.shape[-1] // 256,), Q8K)
+    orc().orc_q8k_quantize(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def ref_q8k_quantize(x):
+    """The reference's own janas_q8k_quantize (compiled quant.c)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(x.shape[:-1] + (x.shape[-1] // 256,), Q8K)
+    lib = RefAttention.lib()
+    lib.janas_q8k_quantize.argtypes = [_vp, _vp, ctypes.c_size_t]
+    lib.janas_q8k_quantize.restype = None
+    lib.janas_q8k_quantize(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def cache_write(k, v, *, cs, sn, n_rot, pos0, kc, vc, kz, vz, k_norm=None,
+                eps=1e-6, v_norm=False, ring=False):
+    """qkv_item's K/V part (model_attn.c:75-146): k, v (n, n_kv, hd) float32
+    are normalized / turned in place and written at eight (kc int8) or
+    sixteen (kc int16) bits into kc, vc (n_kv, cap, hd) and kz, vz
+    (n_kv, cap)."""
+    n, n_kv, hd = k.shape
+    cap = kc.shape[1]
+    wide = kc.dtype == np.int16
+    assert k.dtype == np.float32 and v.dtype == np.float32
+    assert k.flags.c_contiguous and v.flags.c_contiguous
+    cs = np.ascontiguousarray(cs, np.float32)
+    sn = np.ascontiguousarray(sn, np.float32)
+    kn = None if k_norm is None else np.ascontiguousarray(k_norm, np.float32)
+    orc().orc_cache_write(_ptr(k), _ptr(v), _ptr(kn), eps, _ptr(cs), _ptr(sn),
+                          n_rot, 1 if v_norm else 0, n, n_kv, hd, pos0, cap,
+                          1 if ring else 0, 1 if wide else 0, _ptr(kc),
+                          _ptr(vc), _ptr(kz), _ptr(vz))
+
+
+def q_prep(q, *, cs, sn, n_rot, q_norm=None, eps=1e-6):
+    """The query side of qkv_item, in place on q (n, n_head, hd)."""
+    n, n_head, hd = q.shape
+    cs = np.ascontiguousarray(cs, np.float32)
+    sn = np.ascontiguousarray(sn, np.float32)
+    qn = None if q_norm is None else np.ascontiguousarray(q_norm, np.float32)
+    orc().orc_q_prep(_ptr(q), _ptr(qn), eps, _ptr(cs), _ptr(sn), n_rot, n,
+                     n_head, hd)
+
+
+def unrotate_row(row, scale, cs, sn):
+    """unrotate_row (model.c:263-290) on one int8 / int16 row in place;
+    returns the new scale."""
+    sc = np.array([scale], np.float32)
+    cs = np.ascontiguousarray(cs, np.float32)
+    sn = np.ascontiguousarray(sn, np.float32)
+    orc().orc_unrotate_row(_ptr(row), _ptr(sc), row.shape[0], cs.shape[0],
+                           _ptr(cs), _ptr(sn), 1 if row.dtype == np.int16 else 0)
+    return float(sc[0])
+
+
+def cache_shift(k, v, kz, vz, *, keep, drop, n_pos, cs, sn, n_rot,
+                ring=False):
+    """One slot of janas_llm_model_shift (model.c:304-377), in place."""
+    n_kv, cap, hd = k.shape
+    cs = np.ascontiguousarray(cs, np.float32)
+    sn = np.ascontiguousarray(sn, np.float32)
+    rc = orc().orc_cache_shift(_ptr(k), _ptr(v), _ptr(kz), _ptr(vz), n_kv,
+                               hd, cap, 1 if ring else 0,
+                               1 if k.dtype == np.int16 else 0, keep, drop,
+                               n_pos, _ptr(cs), _ptr(sn), n_rot)
+    if rc != 0:
+        raise ValueError("orc_cache_shift rejected the call")
 
 
 class RefAttention:
