@@ -88,6 +88,57 @@ __device__ __forceinline__ uint32_t row_lo(const PrefillArgs &A, uint32_t pos)
     return A.window && pos + 1 > A.window ? pos + 1 - A.window : 0;
 }
 
+/*
+ * The cache's element types as the kernel stages them: 8 consecutive numbers
+ * of a row (a 16-byte LDS store of f16) from their raw bytes. f16 is stored
+ * as it is; int8 and int16 are dequantized with the position's scale into
+ * f16 - the number the cache stands for, at f16's 11 bits.
+ */
+template <int T> struct PElem;
+template <> struct PElem<kF16> {
+    typedef u4 Raw;
+    static constexpr bool SCALED = false;
+    __device__ static Raw load(const void *b, size_t i)
+    {
+        return *(const u4 *)((const uint16_t *)b + i);
+    }
+    __device__ static u4 to_f16(const Raw &r, float) { return r; }
+};
+template <> struct PElem<kI8> {
+    typedef uint2 Raw;
+    static constexpr bool SCALED = true;
+    __device__ static Raw load(const void *b, size_t i)
+    {
+        return *(const uint2 *)((const int8_t *)b + i);
+    }
+    __device__ static u4 to_f16(const Raw &r, float z)
+    {
+        h8 h;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            h[e] = (_Float16)((float)(int8_t)(r.x >> (8 * e)) * z);
+            h[4 + e] = (_Float16)((float)(int8_t)(r.y >> (8 * e)) * z);
+        }
+        return __builtin_bit_cast(u4, h);
+    }
+};
+template <> struct PElem<kI16> {
+    typedef u4 Raw;
+    static constexpr bool SCALED = true;
+    __device__ static Raw load(const void *b, size_t i)
+    {
+        return *(const u4 *)((const int16_t *)b + i);
+    }
+    __device__ static u4 to_f16(const Raw &r, float z)
+    {
+        h8 h;
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            h[e] = (_Float16)((float)(int16_t)(r[e / 2] >> (16 * (e % 2))) * z);
+        return __builtin_bit_cast(u4, h);
+    }
+};
+
 template <int D> struct PShape {
     static constexpr int KP = D + 8;   /* halves a K row in LDS (pitch) */
     static constexpr int VP = D + 16;  /* halves a V row in LDS */
@@ -106,10 +157,11 @@ template <int D> struct PShape {
  * element i of o[c] is column 32 c + 8 (i / 4) + 4 (l / 32) + i % 4 of the
  * lane's row - so the softmax state and the output of a row share a lane.
  */
-template <int D>
+template <int T, int D>
 __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
 {
     using S = PShape<D>;
+    using E = PElem<T>;
     static_assert(S::UPT >= 1 && S::UNITS % (kPWaves * 64) == 0, "tile loads");
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][kTile][S::KP];
     __shared__ __attribute__((aligned(16))) _Float16 sV[2][kTile][S::VP];
@@ -137,6 +189,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
     const uint32_t hi_all = sq.last ? sq.end - 1 : sq.pos0 + jl;
     const uint32_t tfirst = lo_all / kTile, tlast = hi_all / kTile;
     const size_t head_row = (size_t)kvh * sq.cap;
+    const bool ring = A.ring != 0;
 
     /* ---- the lane's row ---- */
     const uint32_t r = r0 + kPRows * w + l32;
@@ -166,26 +219,34 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
        [lo_all, hi_all] read the nearest of the two (masked, but never a row
        the caller has not written); columns past hd read column 0 (their
        products meet zero query columns, or are not stored) ---- */
-    auto load = [&](uint32_t tile, u4 *kr, u4 *vr) {
+    auto load = [&](uint32_t tile, typename E::Raw *kr, typename E::Raw *vr,
+                    float *kz, float *vz) {
 #pragma unroll
         for (int u = 0; u < S::UPT; u++) {
             const uint32_t unit = tid + u * (kPWaves * 64);
             const uint32_t row = unit / S::UPR, cu = unit % S::UPR;
             uint32_t p = tile * kTile + row;
             p = p < lo_all ? lo_all : p > hi_all ? hi_all : p;
-            const size_t cr = head_row + (A.ring ? p % sq.cap : p);
+            if (ring)
+                p %= sq.cap;
+            const size_t cr = head_row + p;
             const uint32_t col = cu * 8 < hd ? cu * 8 : 0;
-            kr[u] = *(const u4 *)((const uint16_t *)sq.k + cr * hd + col);
-            vr[u] = *(const u4 *)((const uint16_t *)sq.v + cr * hd + col);
+            kr[u] = E::load(sq.k, cr * hd + col);
+            vr[u] = E::load(sq.v, cr * hd + col);
+            if constexpr (E::SCALED) {
+                kz[u] = sq.ks[cr];
+                vz[u] = sq.vs[cr];
+            }
         }
     };
-    auto store = [&](int b, const u4 *kr, const u4 *vr) {
+    auto store = [&](int b, const typename E::Raw *kr, const typename E::Raw *vr,
+                     const float *kz, const float *vz) {
 #pragma unroll
         for (int u = 0; u < S::UPT; u++) {
             const uint32_t unit = tid + u * (kPWaves * 64);
             const uint32_t row = unit / S::UPR, cu = unit % S::UPR;
-            *(u4 *)&sK[b][row][cu * 8] = kr[u];
-            *(u4 *)&sV[b][row][cu * 8] = vr[u];
+            *(u4 *)&sK[b][row][cu * 8] = E::to_f16(kr[u], E::SCALED ? kz[u] : 1.0f);
+            *(u4 *)&sV[b][row][cu * 8] = E::to_f16(vr[u], E::SCALED ? vz[u] : 1.0f);
         }
     };
 
@@ -198,15 +259,16 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
         for (int i = 0; i < 16; i++)
             o[c][i] = 0.0f;
 
-    u4 kr[S::UPT], vr[S::UPT];
-    load(tfirst, kr, vr);
-    store(0, kr, vr);
+    typename E::Raw kr[S::UPT], vr[S::UPT];
+    float kz[S::UPT], vz[S::UPT];
+    load(tfirst, kr, vr, kz, vz);
+    store(0, kr, vr, kz, vz);
     __syncthreads();
 
     for (uint32_t tile = tfirst; tile <= tlast; tile++) {
         const int buf = (tile - tfirst) & 1;
         if (tile < tlast)
-            load(tile + 1, kr, vr);
+            load(tile + 1, kr, vr, kz, vz);
         const uint32_t p0 = tile * kTile;
 
         /* scores less the row's maximum so far (the accumulators start at
@@ -297,7 +359,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
         }
         if (tile < tlast) {
             __syncthreads(); /* every wave is done with the other buffer */
-            store(buf ^ 1, kr, vr);
+            store(buf ^ 1, kr, vr, kz, vz);
             __syncthreads();
         }
     }
@@ -328,18 +390,29 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
         }
 }
 
-template <int D>
+template <int T, int D>
 hipError_t launch_d(const PrefillArgs &a, hipStream_t s)
 {
-    hipLaunchKernelGGL((prefill_kernel<D>), dim3(a.n_wg), dim3(512), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(a.n_wg), dim3(512), 0, s, a);
     return hipGetLastError();
+}
+
+template <int T>
+hipError_t launch_t(const PrefillArgs &a, hipStream_t s)
+{
+    if (a.hd <= 64)
+        return launch_d<T, 64>(a, s);
+    if (a.hd <= 128)
+        return launch_d<T, 128>(a, s);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
 
 int prefill_supported(int kv, uint32_t hd)
 {
-    return kv == kF16 && hd >= 8 && hd % 8 == 0 && hd <= 128;
+    return (kv == kF16 || kv == kI8 || kv == kI16) && hd >= 8 && hd % 8 == 0 &&
+           hd <= 128;
 }
 
 uint32_t prefill_row_blocks(uint32_t n, uint32_t group)
@@ -350,12 +423,14 @@ uint32_t prefill_row_blocks(uint32_t n, uint32_t group)
 
 hipError_t launch_prefill(int kv, const PrefillArgs &a, hipStream_t s)
 {
-    if (kv != kF16)
-        return hipErrorInvalidValue;
-    if (a.hd <= 64)
-        return launch_d<64>(a, s);
-    if (a.hd <= 128)
-        return launch_d<128>(a, s);
+    switch (kv) {
+    case kF16:
+        return launch_t<kF16>(a, s);
+    case kI8:
+        return launch_t<kI8>(a, s);
+    case kI16:
+        return launch_t<kI16>(a, s);
+    }
     return hipErrorInvalidValue;
 }
 

@@ -216,8 +216,58 @@ def test_prefill_several_sequences(gpu):
             assert err <= TOL_F16_ABS
 
 
+def quantized(seed, n_kv, cap, hd, wide):
+    """A cache as the engine writes it (model_attn.c:115-145): each row's
+    largest magnitude at 127 (32767), its scale max / 127."""
+    x = cache(seed, n_kv, cap, hd, np.float32)
+    top = np.float32(32767.0 if wide else 127.0)
+    m = np.abs(x).max(axis=2)
+    z = (m / top).astype(np.float32)
+    q = np.rint(x * (top / m)[..., None]).astype(np.int16 if wide else np.int8)
+    return q, z
+
+
+@pytest.mark.parametrize("wide", [False, True])
+@pytest.mark.parametrize("geom", [dict(n_head=32, n_kv=8, hd=128, cap=1024,
+                                       n=1024, pos0=0),
+                                  dict(n_head=12, n_kv=4, hd=64, cap=900,
+                                       n=333, pos0=500, window=300),
+                                  dict(n_head=8, n_kv=1, hd=96, cap=768,
+                                       n=200, pos0=600, window=200,
+                                       ring=True)])
+def test_prefill_quantized_cache(gpu, wide, geom):
+    """int8 / int16 caches with their scales (the engine's own format) on
+    the MFMA path: rows dequantized into f16 as tiles are staged; the bar is
+    the f16 one."""
+    h, kvh, hd, cap = geom["n_head"], geom["n_kv"], geom["hd"], geom["cap"]
+    n, pos0 = geom["n"], geom["pos0"]
+    k, ks = quantized(400 + hd, kvh, cap, hd, wide)
+    v, vs = quantized(401 + hd, kvh, cap, hd, wide)
+    q = normal(402 + hd, n * h * hd).reshape(n, h, hd)
+    kv = janas_amd.KV_I16 if wide else janas_amd.KV_I8
+    out = torch.full((n, h, hd), float("nan"), device=gpu)
+    with Attention(h, kvh, hd, cap) as a:
+        if geom.get("window"):
+            a.set_window(geom["window"])
+        if geom.get("ring"):
+            a.set_ring(True)
+        a.prof_enable(True)
+        a.run_dev(kv, [dict(k=to_dev(k, gpu), v=to_dev(v, gpu),
+                            ks=to_dev(ks, gpu), vs=to_dev(vs, gpu),
+                            q=to_dev(q, gpu), out=out, cap=cap, n=n,
+                            pos0=pos0)], path="prefill")
+        torch.cuda.synchronize()
+        assert prefill_launches(a) == 1
+    ref = orc.run(q, k, v, ks, vs, n_head=h, n_kv=kvh, hd=hd, pos0=pos0,
+                  kv=kv, window=geom.get("window", 0),
+                  ring=geom.get("ring", False), threads=threads(), block=64)
+    err = abs_err(out.cpu().numpy(), ref)
+    print(f"{geom} wide={wide}: max abs err {err:.2e}")
+    assert err <= TOL_F16_ABS
+
+
 def test_prefill_refuses_what_it_has_no_kernel_for(gpu):
-    """int8 caches and head sizes above 128 have no prefill kernel:
+    """f32 caches and head sizes above 128 have no prefill kernel:
     janas_attn_run_dev_prefill says ENOTSUP, janas_attn_run_dev takes the
     split path."""
     h, kvh, hd, cap, n = 4, 2, 256, 300, 100
