@@ -15,17 +15,26 @@
  *               whole GQA group. Row blocks of later tokens (more keys to
  *               see) are dispatched first; consecutive workgroups share a KV
  *               head, so they share an XCD's L2.
- *   key tiles   64 positions of K and V in LDS, two buffers; the next tile
- *               is loaded into registers while this one is computed.
- *   scores      S^T = K . Q^T, v_mfma_f32_16x16x32_f16: A = K rows from LDS,
- *               B = the query in f16, scaled by the score scale times
- *               log2(e) so the weights are exp2(s - max); lane l ends with
- *               row l % 16 at positions 4 (l / 16) + i, the A layout of the
+ *   key tiles   128 positions of K and V in LDS (f16; int8 / int16 caches
+ *               dequantized with their scales as they are staged), two
+ *               buffers; the next tile is loaded into registers while this
+ *               one is computed. 128 rather than 64 positions: the tile's
+ *               fixed costs (barriers, the row maximum's exchange, the
+ *               stores) spread over twice the products (+3 %).
+ *   scores      S^T = K . Q^T on v_mfma_f32_32x32x16_f16: A = K rows from
+ *               LDS, B = the query in f16, scaled by the score scale times
+ *               log2(e) so that the weights are exp2(s - m). Lane l holds
+ *               32 positions of row l % 32 - already the B layout of the
  *               value product.
- *   values      O = P . V with the weights in f16 as they are, V rows read
- *               back transposed with ds_read_b64_tr_b16; f32 accumulation.
+ *   softmax     one lane's row state (maximum m, sum) with a lazy maximum:
+ *               m moves only when a score passes it by more than 8, which
+ *               keeps the weights inside f16 and skips almost every
+ *               rescaling; the accumulators start at -m, so no subtraction.
+ *   values      O^T += V^T . P^T with the weights in f16 as they are, V rows
+ *               read back transposed (ds_read_b64_tr_b16); a row's output
+ *               stays in the lane that holds its softmax state.
  *   masks       only the tiles a row's range cuts; tiles wholly outside
- *               every row's range are skipped.
+ *               every row's range are not visited.
  *   epilogue    O / sum, the output gate sigmoid(g) * o (model_attn.c:
  *               159-170) fused in.
  *
@@ -53,7 +62,8 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 constexpr int kPWaves = 8;                 /* waves a workgroup */
 constexpr int kPRows = 32;                 /* query rows a wave */
 constexpr int kPBlock = kPWaves * kPRows;  /* query rows a workgroup */
-constexpr int kTile = 64;                  /* key positions a tile */
+constexpr int kTile = 128;                 /* key positions a tile */
+constexpr int kNPB = kTile / 32;           /* blocks of 32 positions a tile */
 constexpr float kLog2e = 1.4426950408889634f;
 /* a row's weights are exp2(s - m) against a maximum m that is only moved
    when a score passes it by more than this (so weights stay below 2^8,
@@ -274,16 +284,16 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
         /* scores less the row's maximum so far (the accumulators start at
            -m): 2 blocks of 32 positions */
         const float mref = m == -INFINITY ? 0.0f : m;
-        f16x sacc[2];
+        f16x sacc[kNPB];
 #pragma unroll
-        for (int b = 0; b < 2; b++)
+        for (int b = 0; b < kNPB; b++)
 #pragma unroll
             for (int i = 0; i < 16; i++)
                 sacc[b][i] = -mref;
 #pragma unroll
         for (int s = 0; s < S::KS; s++)
 #pragma unroll
-            for (int b = 0; b < 2; b++) {
+            for (int b = 0; b < kNPB; b++) {
                 const h8 ka = *(const h8 *)&sK[buf][32 * b + l32][16 * s + 8 * g];
                 sacc[b] = mfma(ka, qb[s], sacc[b]);
             }
@@ -292,7 +302,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
         const bool partial = !(rlo <= p0 && rhi >= p0 + kTile - 1);
         if (__any(partial)) {
 #pragma unroll
-            for (int b = 0; b < 2; b++)
+            for (int b = 0; b < kNPB; b++)
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const uint32_t p = p0 + 32 * b + 8 * (i / 4) + 4 * g + i % 4;
@@ -302,7 +312,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
         }
         float mx = -INFINITY;
 #pragma unroll
-        for (int b = 0; b < 2; b++)
+        for (int b = 0; b < kNPB; b++)
 #pragma unroll
             for (int i = 0; i < 16; i++)
                 mx = fmaxf(mx, sacc[b][i]);
@@ -316,7 +326,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
             m = move ? mref + mx : m;
             lsum *= alpha;
 #pragma unroll
-            for (int b = 0; b < 2; b++)
+            for (int b = 0; b < kNPB; b++)
 #pragma unroll
                 for (int i = 0; i < 16; i++)
                     sacc[b][i] -= sh;
@@ -329,10 +339,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
 
         /* weights in f16, the PV operands: k-step ks holds positions
            32 (ks / 2) + 16 (ks % 2) + 8 (e / 4) + 4 (l / 32) + e % 4 */
-        h8 pa[4];
+        h8 pa[2 * kNPB];
         float ls = 0.0f;
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
+        for (int ks = 0; ks < 2 * kNPB; ks++) {
 #pragma unroll
             for (int e = 0; e < 8; e++)
                 pa[ks][e] = (_Float16)__builtin_amdgcn_exp2f(sacc[ks / 2][8 * (ks % 2) + e]);
@@ -346,7 +356,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
 
         /* O^T += V^T . P^T */
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
+        for (int ks = 0; ks < 2 * kNPB; ks++) {
             const uint32_t tr = 16 * ks + 4 * g + (l16 >> 2);
 #pragma unroll
             for (int c = 0; c < S::CT; c++) {
