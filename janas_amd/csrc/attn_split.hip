@@ -13,11 +13,10 @@
  *   split kernel   one workgroup (8 waves of 64) per (sequence, KV head,
  *                  chunk, tile of 16 query rows); a query row is a (token,
  *                  query head of the KV head's group), so every K/V row of
- *                  the chunk is read once for the whole GQA group. The whole
- *                  chunk is in flight at once: wave w loads positions
- *                  32 w .. 32 w + 31 of K and V with contiguous 16-byte loads
- *                  (V after the query barrier, so the query's loads are not
- *                  queued behind it), stages them through its own LDS region
+ *                  the chunk is read once for the whole GQA group. Wave w
+ *                  loads positions 32 w .. 32 w + 31 of K at once, then of V
+ *                  as soon as its K is in, with contiguous 16-byte loads,
+ *                  stages them through its own LDS region
  *                  into MFMA operand order, and computes a one-shot softmax
  *                  over its 32 positions; the 8 waves' partials are combined
  *                  in LDS in a fixed order into the chunk's exact partial.
