@@ -61,8 +61,7 @@ size_t janas_attn_part_bytes(uint32_t n_head, uint32_t n_head_kv,
 
 /* attention.h:62-64 - NULL on a bad geometry (n_head_kv 0, n_head not a
    multiple of it, head_dim not a multiple of 8 or above 512, n_threads < 1),
-   when the device lacks memory, or when no device is there. head_dim above
-   256 is accepted by the reference and rejected here for now (NULL). */
+   when the device lacks memory, or when no device is there. */
 struct janas_attn *janas_attn_create(uint32_t n_head, uint32_t n_head_kv,
                                      uint32_t head_dim, uint32_t n_ctx,
                                      int n_threads, int scores);
@@ -165,7 +164,9 @@ int janas_attn_run_dev(struct janas_attn *a, int kv_type, int gate_mode,
                        const struct janas_attn_seq *seqs, uint32_t n_seqs,
                        void *stream);
 
-/* The same, always through the split-KV path (any n). */
+/* The same, always through the split-KV path (any n). int8, int16 and f16
+   caches take head_dim up to 512, f32 caches up to 128
+   (JANAS_ATTN_ENOTSUP above). */
 int janas_attn_run_dev_split(struct janas_attn *a, int kv_type, int gate_mode,
                              const struct janas_attn_seq *seqs,
                              uint32_t n_seqs, void *stream);

@@ -350,8 +350,6 @@ extern "C" struct janas_attn *janas_attn_create(uint32_t n_head,
     if (n_head_kv == 0 || n_head % n_head_kv || head_dim % 8 ||
         head_dim > 512 || n_threads < 1)
         return nullptr;
-    if (head_dim > 256)
-        return nullptr; /* no kernel instance yet */
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) {
         (void)hipGetLastError();

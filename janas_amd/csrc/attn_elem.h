@@ -1,0 +1,199 @@
+/*
+ * attn_elem.h - device helpers shared by the split kernels (attn_split.hip,
+ * attn_wide.hip): vector types, the MFMA and transposed-LDS wrappers, how a
+ * cached element type becomes exact f16 planes, the XCD-aware workgroup
+ * order and a token's first visible position. Internal, device code only.
+ */
+#ifndef JANAS_AMD_ATTN_ELEM_H
+#define JANAS_AMD_ATTN_ELEM_H
+
+#include <math.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime.h>
+
+#include "attn_kernels.h"
+
+namespace janas {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+/* 16 bytes as a native vector (HIP's uint4 is a struct, which keeps large
+   arrays of it out of registers) */
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRows = 16;     /* query rows a workgroup */
+
+__device__ __forceinline__ f4 mfma(h8 a, h8 b, f4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+/*
+ * ds_read_b64_tr_b16: within each group of 16 lanes, lane k supplies the
+ * address of 4 halves; lane l receives half l % 4 of the 8-byte pieces of
+ * lanes (l % 16) / 4 + 4 i, i = 0..3. With lane k pointing at
+ * row base + k / 4, column c0 + 4 (k % 4) of a row-major tile, lane l gets
+ * rows base .. base + 3 of column c0 + l % 16: four positions of one value
+ * column, the B layout of the PV product.
+ */
+__device__ __forceinline__ h4 lds_read_tr(const _Float16 *p)
+{
+    s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s4 *)p);
+    return __builtin_bit_cast(h4, v);
+}
+
+/* x = hi + lo, both f16; x already scaled into f16's normal range */
+__device__ __forceinline__ void split_hl(float x, _Float16 &hi, _Float16 &lo)
+{
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+/* ---- element types of the cache -------------------------------------- */
+
+/*
+ * Elem<T>: how 8 consecutive numbers of a cached row become f16 planes
+ * whose sum is the number exactly (planes8).
+ */
+template <int T> struct Elem;
+
+template <> struct Elem<kF16> {
+    static constexpr int bytes = 2, planes = 1;
+    struct Raw { uint4 a; };
+    __device__ static Raw load8(const void *b, size_t i)
+    {
+        return Raw{*(const uint4 *)((const uint16_t *)b + i)};
+    }
+    __device__ static void planes8(const Raw &r, h8 *p)
+    {
+        p[0] = __builtin_bit_cast(h8, r.a);
+    }
+};
+
+template <> struct Elem<kI8> {
+    static constexpr int bytes = 1, planes = 1;
+    struct Raw { uint2 a; };
+    __device__ static Raw load8(const void *b, size_t i)
+    {
+        return Raw{*(const uint2 *)((const int8_t *)b + i)};
+    }
+    __device__ static h8 widen(uint32_t lo, uint32_t hi)
+    {
+        h8 r;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            r[e] = (_Float16)(int)(int8_t)(lo >> (8 * e));
+            r[4 + e] = (_Float16)(int)(int8_t)(hi >> (8 * e));
+        }
+        return r;
+    }
+    __device__ static void planes8(const Raw &r, h8 *p)
+    {
+        p[0] = widen(r.a.x, r.a.y);
+    }
+};
+
+template <> struct Elem<kI16> {
+    static constexpr int bytes = 2, planes = 2;
+    struct Raw { uint4 a; };
+    __device__ static Raw load8(const void *b, size_t i)
+    {
+        return Raw{*(const uint4 *)((const int16_t *)b + i)};
+    }
+    /* x = 256 (x >> 8) + (x & 255): both parts exact in f16 */
+    __device__ static void split(uint4 u, h8 &hi, h8 &lo)
+    {
+        uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            int x = (int)(int16_t)(w[e / 2] >> (16 * (e % 2)));
+            hi[e] = (_Float16)(float)((x >> 8) * 256);
+            lo[e] = (_Float16)(x & 255);
+        }
+    }
+    __device__ static void planes8(const Raw &r, h8 *p) { split(r.a, p[0], p[1]); }
+};
+
+template <> struct Elem<kF32> {
+    static constexpr int bytes = 4, planes = 2;
+    struct Raw { uint4 a, b; };
+    __device__ static Raw load8(const void *b, size_t i)
+    {
+        const uint4 *s = (const uint4 *)((const float *)b + i);
+        return Raw{s[0], s[1]};
+    }
+    __device__ static void planes8(const Raw &r, h8 *p)
+    {
+        uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            _Float16 hi, lo;
+            split_hl(__builtin_bit_cast(float, w[e]), hi, lo);
+            p[0][e] = hi;
+            p[1][e] = lo;
+        }
+    }
+};
+
+/* Which plane pairs enter a product: the low parts of both sides are
+   dropped only when both are true residuals (f32 against the split query
+   or weights), where their product is below 2^-22 of the sum. */
+template <int T> __device__ constexpr bool use_pair(int data_plane, int x_plane)
+{
+    return !(T == kF32 && data_plane == 1 && x_plane == 1);
+}
+
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n)
+{
+    /* blocks are dealt to the 8 XCDs round robin: give each XCD a
+       contiguous run of logical ids, so that the row tiles of one chunk
+       (consecutive ids) share an L2 */
+    uint32_t x = bid % 8, k = bid / 8, q = n / 8, r = n % 8;
+    return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
+}
+
+constexpr int kBlk = 1024 + 32;  /* LDS bytes of a kilobyte of rows */
+
+/* LDS byte offset of byte b of rows stored a kilobyte at a time, each
+   followed by 32 bytes of padding (spreads the rows over the banks) */
+__device__ __forceinline__ uint32_t blk_off(uint32_t b)
+{
+    return (b >> 10) * kBlk + (b & 1023);
+}
+
+/*
+ * The 16-byte unit of a cached row that starts at byte cb (units past the
+ * row's rowb bytes read its first unit). An int8 row of 8 mod 16 bytes ends
+ * inside its last unit: that unit is read 8 bytes earlier (back), so the
+ * load stays inside the row - and inside the buffer at the cache's last
+ * row - and unit_fix() swaps its halves into place: the first 8 bytes are
+ * the row's last 8, the other 8 are finite numbers of the same row that
+ * land in columns past hd (multiplied by zero query columns, or not stored).
+ */
+__device__ __forceinline__ uint32_t unit_at(uint32_t cb, uint32_t rowb, bool &back)
+{
+    const uint32_t c = cb < rowb ? cb : 0;
+    back = c + 16 > rowb;
+    return back ? c - 8 : c;
+}
+
+__device__ __forceinline__ u4 unit_fix(u4 x, bool back)
+{
+    return back ? u4{x.z, x.w, x.x, x.y} : x;
+}
+
+__device__ __forceinline__ uint32_t row_lo(const SplitArgs &A, uint32_t pos)
+{
+    return A.window && pos + 1 > A.window ? pos + 1 - A.window : 0;
+}
+
+}  // namespace
+}  // namespace janas
+
+#endif

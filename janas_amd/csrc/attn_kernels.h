@@ -1,6 +1,7 @@
 /*
  * attn_kernels.h - launch descriptors shared by the host API (attn_api.cpp)
- * and the HIP kernels (attn_split.hip, attn_prefill.hip). Internal: not part
+ * and the HIP kernels (attn_split.hip, attn_wide.hip, attn_prefill.hip,
+ * attn_cache.hip). Internal: not part
  * of the C ABI (include/janas_attn.h).
  */
 #ifndef JANAS_AMD_ATTN_KERNELS_H
@@ -101,6 +102,9 @@ hipError_t launch_merge(const SplitArgs &a, uint32_t n_wg, hipStream_t s);
 /* 1 when the split kernel has an instance for this element type and
    padded head size. */
 int split_supported(int kv, uint32_t hd);
+/* attn_wide.hip: the split kernel for head sizes 264 .. 512 (8- and 16-bit
+   caches); launch_split hands those to it. */
+hipError_t launch_wide(int kv, const SplitArgs &a, hipStream_t s);
 
 /* attn_cache.hip */
 hipError_t launch_rows(const RowArgs &a, hipStream_t s);

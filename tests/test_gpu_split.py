@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import janas_amd
-from attn_helpers import (KV_F16, KV_F32, TOL_F16_ABS, TOL_F32_REL,
+from attn_helpers import (KV_F16, KV_F32, KV_I8, TOL_F16_ABS, TOL_F32_REL,
                           TOL_FLOAT_ABS, abs_err, config, oracle_out, rel_err)
 from cases import CASES, KV_I16, call_kwargs, make_inputs
 from janas_amd import Attention
@@ -17,10 +17,8 @@ from oracle import orc
 pytestmark = pytest.mark.gpu
 
 MAX_BLOCK = janas_amd.MAX_BLOCK
-# head_dim above 256 (Gemma 4's 512) has no kernel instance yet:
-# janas_attn_create returns NULL for it, as documented in include/janas_attn.h
-SUPPORTED = sorted(n for n in CASES if CASES[n]["hd"] <= 256)
-UNSUPPORTED = sorted(n for n in CASES if CASES[n]["hd"] > 256)
+# every golden case, Gemma 4's head_dim 512 included (the wide kernel)
+SUPPORTED = sorted(CASES)
 
 
 def to_dev(x, device):
@@ -95,7 +93,8 @@ def test_dropin_device_matches_closed_form(name, gpu):
 
 @pytest.mark.parametrize("name", ["i8_8x1x128_p250_n17", "i8_4x2x64_p0_n64",
                                   "i16_4x1x64_p1030_n5_w64_ring",
-                                  "i8_4x1x64_p600_n8_w300"])
+                                  "i8_4x1x64_p600_n8_w300",
+                                  "i16_2x1x512_p100_n3"])
 def test_dropin_block_equals_tokens(name, gpu):
     """A token's result does not depend on the block it runs in."""
     c = CASES[name]
@@ -109,13 +108,6 @@ def test_dropin_block_equals_tokens(name, gpu):
         for j in range(n):
             a.run(q[j:j + 1], k, ks, v, vs, 1, pos0 + j, one[j:j + 1])
     assert torch.equal(blk.view(torch.int32), one.view(torch.int32))
-
-
-@pytest.mark.parametrize("name", UNSUPPORTED)
-def test_head_dim_above_256_refused(name, gpu):
-    c = CASES[name]
-    with pytest.raises(ValueError):
-        Attention(c["n_head"], c["n_kv"], c["hd"], c["n_ctx"])
 
 
 def seq_dev(cfg, s, gpu):
@@ -210,3 +202,30 @@ def test_f32_cache_equals_int8_unit_scales(gpu):
         err = abs_err(out, ref)
         print(f"kv {kv}: |gpu - reference int8| = {err:.2e}")
         assert err <= TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+
+
+@pytest.mark.parametrize("hd", [72, 200])
+def test_int8_rows_of_8_mod_16_bytes(hd, gpu):
+    """int8 rows whose length is 8 mod 16 bytes: the last 16-byte unit of a
+    row is read 8 bytes early (never past the buffer at the cache's last
+    row) and its halves put back; decode at the cache's last position."""
+    from cases import uniform
+    h, kvh, cap = 8, 2, 777
+    cells, rows = kvh * cap * hd, kvh * cap
+    k = uniform(7001 + hd, cells, -127, 127).astype(np.int32).astype(np.int8)
+    v = uniform(7002 + hd, cells, -127, 127).astype(np.int32).astype(np.int8)
+    ks = uniform(7003 + hd, rows, 0.001, 0.02).reshape(kvh, cap)
+    vs = uniform(7004 + hd, rows, 0.001, 0.02).reshape(kvh, cap)
+    q = uniform(7005 + hd, 2 * h * hd, -3, 3).reshape(2, h, hd)
+    k, v = k.reshape(kvh, cap, hd), v.reshape(kvh, cap, hd)
+    ref = orc.run(q, k, v, ks, vs, n_head=h, n_kv=kvh, hd=hd, pos0=cap - 2,
+                  kv=KV_I8, threads=4)
+    d = dict(k=to_dev(k, gpu), v=to_dev(v, gpu), ks=to_dev(ks, gpu),
+             vs=to_dev(vs, gpu), q=to_dev(q, gpu), cap=cap, n=2, pos0=cap - 2)
+    d["out"] = torch.zeros(d["q"].shape, dtype=torch.float32, device=gpu)
+    with Attention(h, kvh, hd, cap) as a:
+        a.run_dev(KV_I8, [d], path="split")
+        torch.cuda.synchronize()
+    err = abs_err(d["out"].cpu().numpy(), ref)
+    print(f"int8 hd {hd}: max abs err {err:.2e}")
+    assert err <= TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
