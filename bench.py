@@ -302,7 +302,7 @@ def main():
                      "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": traffic_from_profiles("prefill_kernel_8k"),
-                     "kernel": "prefill_kernel<f16, 128>"},
+                     "kernel": "prefill_dma_kernel<128>"},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_decode_baseline(w)

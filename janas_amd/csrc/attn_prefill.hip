@@ -15,12 +15,18 @@
  *               whole GQA group. Row blocks of later tokens (more keys to
  *               see) are dispatched first; consecutive workgroups share a KV
  *               head, so they share an XCD's L2.
- *   key tiles   128 positions of K and V in LDS (f16; int8 / int16 caches
- *               dequantized with their scales as they are staged), two
- *               buffers; the next tile is loaded into registers while this
- *               one is computed. 128 rather than 64 positions: the tile's
- *               fixed costs (barriers, the row maximum's exchange, the
- *               stores) spread over twice the products (+3 %).
+ *   key tiles   128 positions of K and V in LDS, two buffers; the next
+ *               tile is loaded while this one is computed. 128 rather than
+ *               64 positions: the tile's fixed costs (barriers, the row
+ *               maximum's exchange) spread over twice the products (+3 %).
+ *               Two kernels differ only in how a tile reaches LDS:
+ *               prefill_dma_kernel (f16, head sizes 72..128) loads it
+ *               straight from memory into XOR-swizzled LDS rows
+ *               (global_load_lds_dwordx4; one barrier a tile) and keeps its
+ *               operand reads a k-step ahead of the products;
+ *               prefill_kernel (int8 / int16, dequantized with their scales
+ *               as they are staged, and head sizes up to 64) goes through
+ *               registers into padded rows.
  *   scores      S^T = K . Q^T on v_mfma_f32_32x32x16_f16: A = K rows from
  *               LDS, B = the query in f16, scaled by the score scale times
  *               log2(e) so that the weights are exp2(s - m). Lane l holds
@@ -161,29 +167,35 @@ template <int D> struct PShape {
 };
 
 /*
+ * What a workgroup and a lane work on (shared by both kernels below).
  * Lane l of wave w owns query row r0 + 32 w + l % 32 (half its scores sit
  * in lane l ^ 32). Scores S^T = K . Q^T: element i of sacc[b] is position
  * p0 + 32 b + 8 (i / 4) + 4 (l / 32) + i % 4. Outputs O^T = V^T . P^T:
  * element i of o[c] is column 32 c + 8 (i / 4) + 4 (l / 32) + i % 4 of the
  * lane's row - so the softmax state and the output of a row share a lane.
  */
-template <int T, int D>
-__global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
-{
-    using S = PShape<D>;
-    using E = PElem<T>;
-    static_assert(S::UPT >= 1 && S::UNITS % (kPWaves * 64) == 0, "tile loads");
-    __shared__ __attribute__((aligned(16))) _Float16 sK[2][kTile][S::KP];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[2][kTile][S::VP];
+struct PBlock {
+    const SeqDesc *sq;
+    uint32_t lo_all, hi_all;   /* positions any row of the block sees */
+    uint32_t tfirst, tlast;    /* key tiles visited */
+    size_t head_row;           /* the KV head's first cache row */
+    bool rok;                  /* the lane's row exists */
+    uint32_t rj, rh;           /* its token and query head */
+    uint32_t rlo, rhi;         /* the positions it sees */
+};
 
-    const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const uint32_t g = lane >> 5, l32 = lane & 31, l16 = lane & 15;
+__device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
+{
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t l32 = lane & 31;
     const uint32_t id = xcd_remap(blockIdx.x, gridDim.x);
     uint32_t si = 0;
     while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
         si++;
-    const SeqDesc &sq = A.seq[si];
-    const uint32_t G = A.group, hd = A.hd;
+    PBlock P;
+    P.sq = &A.seq[si];
+    const SeqDesc &sq = *P.sq;
+    const uint32_t G = A.group;
     const uint32_t R = sq.n * G;
     const uint32_t nrb = (R + kPBlock - 1) / kPBlock;
     const uint32_t local = id - sq.wg0;
@@ -194,52 +206,268 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
     /* the block's rows see [lo(first token), hi(last token)] */
     const uint32_t rows_here = R - r0 < kPBlock ? R - r0 : kPBlock;
     const uint32_t jf = r0 / G, jl = (r0 + rows_here - 1) / G;
-    const uint32_t lo_all = row_lo(A, sq.pos0 + jf);
+    P.lo_all = row_lo(A, sq.pos0 + jf);
     /* with set_last's bounds any token may see up to the call's end */
-    const uint32_t hi_all = sq.last ? sq.end - 1 : sq.pos0 + jl;
-    const uint32_t tfirst = lo_all / kTile, tlast = hi_all / kTile;
-    const size_t head_row = (size_t)kvh * sq.cap;
-    const bool ring = A.ring != 0;
+    P.hi_all = sq.last ? sq.end - 1 : sq.pos0 + jl;
+    P.tfirst = P.lo_all / kTile;
+    P.tlast = P.hi_all / kTile;
+    P.head_row = (size_t)kvh * sq.cap;
 
-    /* ---- the lane's row ---- */
     const uint32_t r = r0 + kPRows * w + l32;
-    const bool rok = r < R;
-    const uint32_t rj = (rok ? r : r0) / G;
-    const uint32_t rh = kvh * G + (rok ? r : r0) % G;
-    const uint32_t rlo = rok ? row_lo(A, sq.pos0 + rj) : 1;
-    const uint32_t rhi = rok ? (sq.last ? sq.last[rj] : sq.pos0 + rj) : 0;
-    h8 qb[S::KS];
-    {
-        const float *qrow = sq.q + ((size_t)rj * A.n_head + rh) * hd;
-        const float f = A.scale * kLog2e;
+    P.rok = r < R;
+    P.rj = (P.rok ? r : r0) / G;
+    P.rh = kvh * G + (P.rok ? r : r0) % G;
+    P.rlo = P.rok ? row_lo(A, sq.pos0 + P.rj) : 1;
+    P.rhi = P.rok ? (sq.last ? sq.last[P.rj] : sq.pos0 + P.rj) : 0;
+    return P;
+}
+
+/* the lane's query row in f16, scaled by the score scale times log2(e):
+   the B operands of the score product */
+template <int D>
+__device__ __forceinline__ void load_query(const PrefillArgs &A, const PBlock &P,
+                                           h8 *qb)
+{
+    const uint32_t g = (threadIdx.x & 63) >> 5, hd = A.hd;
+    const float *qrow = P.sq->q + ((size_t)P.rj * A.n_head + P.rh) * hd;
+    const float f = A.scale * kLog2e;
 #pragma unroll
-        for (int s = 0; s < S::KS; s++) {
-            const uint32_t c = 16 * s + 8 * g;
-            const bool cok = rok && c < hd;
-            const float4 x0 = *(const float4 *)(qrow + (cok ? c : 0));
-            const float4 x1 = *(const float4 *)(qrow + (cok ? c + 4 : 0));
-            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    for (int s = 0; s < D / 16; s++) {
+        const uint32_t c = 16 * s + 8 * g;
+        const bool cok = P.rok && c < hd;
+        const float4 x0 = *(const float4 *)(qrow + (cok ? c : 0));
+        const float4 x1 = *(const float4 *)(qrow + (cok ? c + 4 : 0));
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-                qb[s][e] = (_Float16)(cok ? xs[e] * f : 0.0f);
-        }
+        for (int e = 0; e < 8; e++)
+            qb[s][e] = (_Float16)(cok ? xs[e] * f : 0.0f);
+    }
+}
+
+/*
+ * One key tile of 128 positions from p0 for the lane's row: the scores,
+ * the masks, the lazy-maximum softmax and the value product. kop(s, b) is
+ * the A operand of score k-step s for positions 32 b .. 32 b + 31 (K rows
+ * 32 b + l % 32, columns 16 s + 8 (l / 32) .. + 7); vop(ks, c) the A operand
+ * of value k-step ks for columns 32 c .. 32 c + 31 (positions 16 ks +
+ * 4 (l / 32) + 0..3 and + 8 of column 32 c + l % 32).
+ */
+template <int D, bool PIPE, class KOp, class VOp>
+__device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8 *qb,
+                                          float &m, float &lsum, f16x *o,
+                                          KOp kop, VOp vop)
+{
+    constexpr int KS = D / 16, CT = D / 32;
+    const uint32_t g = (threadIdx.x & 63) >> 5;
+    /* scores less the row's maximum so far (the accumulators start at
+       -m): kNPB blocks of 32 positions */
+    const float mref = m == -INFINITY ? 0.0f : m;
+    f16x sacc[kNPB];
+#pragma unroll
+    for (int b = 0; b < kNPB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            sacc[b][i] = -mref;
+    /* PIPE: the operands of k-step s + 1 are asked for before the products
+       of step s, so the LDS latency hides behind them (32 more registers) */
+    if constexpr (!PIPE) {
+#pragma unroll
+        for (int s = 0; s < KS; s++)
+#pragma unroll
+            for (int b = 0; b < kNPB; b++)
+                sacc[b] = mfma(kop(s, b), qb[s], sacc[b]);
+    } else {
+    h8 ka[2][kNPB];
+#pragma unroll
+    for (int b = 0; b < kNPB; b++)
+        ka[0][b] = kop(0, b);
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+        if (s + 1 < KS)
+#pragma unroll
+            for (int b = 0; b < kNPB; b++)
+                ka[(s + 1) & 1][b] = kop(s + 1, b);
+#pragma unroll
+        for (int b = 0; b < kNPB; b++)
+            sacc[b] = mfma(ka[s & 1][b], qb[s], sacc[b]);
+    }
+    /* keep that order: the scheduler would otherwise sink every read to
+       just before its product */
+    __builtin_amdgcn_sched_group_barrier(0x100, kNPB, 0);
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+        if (s + 1 < KS)
+            __builtin_amdgcn_sched_group_barrier(0x100, kNPB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kNPB, 0);
+    }
     }
 
-    /* ---- a tile's K and V: thread t's units t + 512 u. Positions outside
-       [lo_all, hi_all] read the nearest of the two (masked, but never a row
-       the caller has not written); columns past hd read column 0 (their
-       products meet zero query columns, or are not stored) ---- */
+    /* masks, only where a row of the wave sees part of the tile */
+    const bool partial = !(P.rlo <= p0 && P.rhi >= p0 + kTile - 1);
+    if (__any(partial)) {
+#pragma unroll
+        for (int b = 0; b < kNPB; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t p = p0 + 32 * b + 8 * (i / 4) + 4 * g + i % 4;
+                if (p < P.rlo || p > P.rhi)
+                    sacc[b][i] = -INFINITY;
+            }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < kNPB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            mx = fmaxf(mx, sacc[b][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    /* move m when the row has none yet, or a score passed it by more than
+       the slack */
+    const bool move = m == -INFINITY ? mx != -INFINITY : mx > kSlack;
+    if (__any(move)) {
+        const float sh = move ? mx : 0.0f;
+        const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-sh);
+        m = move ? mref + mx : m;
+        lsum *= alpha;
+#pragma unroll
+        for (int b = 0; b < kNPB; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                sacc[b][i] -= sh;
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                o[c][i] *= alpha;
+    }
+
+    /* weights in f16, the PV operands: k-step ks holds positions
+       32 (ks / 2) + 16 (ks % 2) + 8 (e / 4) + 4 (l / 32) + e % 4 */
+    h8 pa[2 * kNPB];
+    float ls = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 2 * kNPB; ks++) {
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            pa[ks][e] = (_Float16)__builtin_amdgcn_exp2f(sacc[ks / 2][8 * (ks % 2) + e]);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+            ls = __builtin_amdgcn_fdot2(h2{pa[ks][e], pa[ks][e + 1]},
+                                        h2{(_Float16)1.0f, (_Float16)1.0f},
+                                        ls, false);
+    }
+    lsum += ls;
+
+    /* O^T += V^T . P^T (PIPE: operands one k-step ahead) */
+    if constexpr (!PIPE) {
+#pragma unroll
+        for (int ks = 0; ks < 2 * kNPB; ks++)
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+                o[c] = mfma(vop(ks, c), pa[ks], o[c]);
+        return;
+    }
+    h8 va[2][CT];
+#pragma unroll
+    for (int c = 0; c < CT; c++)
+        va[0][c] = vop(0, c);
+#pragma unroll
+    for (int ks = 0; ks < 2 * kNPB; ks++) {
+        if (ks + 1 < 2 * kNPB)
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+                va[(ks + 1) & 1][c] = vop(ks + 1, c);
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+            o[c] = mfma(va[ks & 1][c], pa[ks], o[c]);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * CT, 1);
+#pragma unroll
+    for (int ks = 0; ks < 2 * kNPB; ks++) {
+        if (ks + 1 < 2 * kNPB)
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * CT, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, CT, 1);
+    }
+}
+
+/* out = sums / weights, gated */
+template <int D>
+__device__ __forceinline__ void write_out(const PrefillArgs &A, const PBlock &P,
+                                          float lsum, const f16x *o)
+{
+    const uint32_t g = (threadIdx.x & 63) >> 5, hd = A.hd;
+    const SeqDesc &sq = *P.sq;
+    const float lt = lsum + __shfl_xor(lsum, 32, 64);
+    if (!P.rok)
+        return;
+    const float inv = 1.0f / lt;
+    const size_t obase = ((size_t)P.rj * A.n_head + P.rh) * hd;
+#pragma unroll
+    for (int c = 0; c < D / 32; c++)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const uint32_t col = 32 * c + 8 * q4 + 4 * g;
+            if (col >= hd)
+                continue;
+            float x[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                x[e] = o[c][4 * q4 + e] * inv;
+                if (A.gate_mode == kGateElem)
+                    x[e] *= 1.0f / (1.0f + expf(-sq.gate[obase + col + e]));
+                else if (A.gate_mode == kGateHead)
+                    x[e] *= 1.0f / (1.0f + expf(-sq.gate[(size_t)P.rj * A.n_head + P.rh]));
+            }
+            *(float4 *)(sq.out + obase + col) = float4{x[0], x[1], x[2], x[3]};
+        }
+}
+
+/* the tile position a row of the tile reads: outside [lo_all, hi_all] the
+   nearest of the two (masked, but never a row the caller has not written),
+   a ring's row modulo its size */
+__device__ __forceinline__ size_t cache_row(const PBlock &P, uint32_t cap, bool ring,
+                                            uint32_t p)
+{
+    p = p < P.lo_all ? P.lo_all : p > P.hi_all ? P.hi_all : p;
+    if (ring)
+        p %= cap;
+    return P.head_row + p;
+}
+
+/*
+ * The kernel for int8 / int16 caches (dequantized with their scales as
+ * tiles are staged) and head sizes up to 64: each thread loads its units
+ * of the next tile into registers while this tile is computed, then stores
+ * them into padded LDS rows (K pitch D + 8, V pitch D + 16 halves).
+ */
+template <int T, int D>
+__global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
+{
+    using S = PShape<D>;
+    using E = PElem<T>;
+    static_assert(S::UPT >= 1 && S::UNITS % (kPWaves * 64) == 0, "tile loads");
+    __shared__ __attribute__((aligned(16))) _Float16 sK[2][kTile][S::KP];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[2][kTile][S::VP];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t g = lane >> 5, l32 = lane & 31, l16 = lane & 15;
+    const PBlock P = block_of(A);
+    const SeqDesc &sq = *P.sq;
+    const uint32_t hd = A.hd;
+    const bool ring = A.ring != 0;
+    h8 qb[S::KS];
+    load_query<D>(A, P, qb);
+
+    /* ---- a tile's K and V: thread t's units t + 512 u; columns past hd
+       read column 0 (their products meet zero query columns, or are not
+       stored) ---- */
     auto load = [&](uint32_t tile, typename E::Raw *kr, typename E::Raw *vr,
                     float *kz, float *vz) {
 #pragma unroll
         for (int u = 0; u < S::UPT; u++) {
             const uint32_t unit = tid + u * (kPWaves * 64);
             const uint32_t row = unit / S::UPR, cu = unit % S::UPR;
-            uint32_t p = tile * kTile + row;
-            p = p < lo_all ? lo_all : p > hi_all ? hi_all : p;
-            if (ring)
-                p %= sq.cap;
-            const size_t cr = head_row + p;
+            const size_t cr = cache_row(P, sq.cap, ring, tile * kTile + row);
             const uint32_t col = cu * 8 < hd ? cu * 8 : 0;
             kr[u] = E::load(sq.k, cr * hd + col);
             vr[u] = E::load(sq.v, cr * hd + col);
@@ -271,139 +499,168 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
 
     typename E::Raw kr[S::UPT], vr[S::UPT];
     float kz[S::UPT], vz[S::UPT];
-    load(tfirst, kr, vr, kz, vz);
+    load(P.tfirst, kr, vr, kz, vz);
     store(0, kr, vr, kz, vz);
     __syncthreads();
 
-    for (uint32_t tile = tfirst; tile <= tlast; tile++) {
-        const int buf = (tile - tfirst) & 1;
-        if (tile < tlast)
+    for (uint32_t tile = P.tfirst; tile <= P.tlast; tile++) {
+        const int buf = (tile - P.tfirst) & 1;
+        if (tile < P.tlast)
             load(tile + 1, kr, vr, kz, vz);
-        const uint32_t p0 = tile * kTile;
-
-        /* scores less the row's maximum so far (the accumulators start at
-           -m): 2 blocks of 32 positions */
-        const float mref = m == -INFINITY ? 0.0f : m;
-        f16x sacc[kNPB];
-#pragma unroll
-        for (int b = 0; b < kNPB; b++)
-#pragma unroll
-            for (int i = 0; i < 16; i++)
-                sacc[b][i] = -mref;
-#pragma unroll
-        for (int s = 0; s < S::KS; s++)
-#pragma unroll
-            for (int b = 0; b < kNPB; b++) {
-                const h8 ka = *(const h8 *)&sK[buf][32 * b + l32][16 * s + 8 * g];
-                sacc[b] = mfma(ka, qb[s], sacc[b]);
-            }
-
-        /* masks, only where a row of the wave sees part of the tile */
-        const bool partial = !(rlo <= p0 && rhi >= p0 + kTile - 1);
-        if (__any(partial)) {
-#pragma unroll
-            for (int b = 0; b < kNPB; b++)
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const uint32_t p = p0 + 32 * b + 8 * (i / 4) + 4 * g + i % 4;
-                    if (p < rlo || p > rhi)
-                        sacc[b][i] = -INFINITY;
-                }
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int b = 0; b < kNPB; b++)
-#pragma unroll
-            for (int i = 0; i < 16; i++)
-                mx = fmaxf(mx, sacc[b][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        /* move m when the row has none yet, or a score passed it by more
-           than the slack */
-        const bool move = m == -INFINITY ? mx != -INFINITY : mx > kSlack;
-        if (__any(move)) {
-            const float sh = move ? mx : 0.0f;
-            const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-sh);
-            m = move ? mref + mx : m;
-            lsum *= alpha;
-#pragma unroll
-            for (int b = 0; b < kNPB; b++)
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    sacc[b][i] -= sh;
-#pragma unroll
-            for (int c = 0; c < S::CT; c++)
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    o[c][i] *= alpha;
-        }
-
-        /* weights in f16, the PV operands: k-step ks holds positions
-           32 (ks / 2) + 16 (ks % 2) + 8 (e / 4) + 4 (l / 32) + e % 4 */
-        h8 pa[2 * kNPB];
-        float ls = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < 2 * kNPB; ks++) {
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                pa[ks][e] = (_Float16)__builtin_amdgcn_exp2f(sacc[ks / 2][8 * (ks % 2) + e]);
-#pragma unroll
-            for (int e = 0; e < 8; e += 2)
-                ls = __builtin_amdgcn_fdot2(h2{pa[ks][e], pa[ks][e + 1]},
-                                            h2{(_Float16)1.0f, (_Float16)1.0f},
-                                            ls, false);
-        }
-        lsum += ls;
-
-        /* O^T += V^T . P^T */
-#pragma unroll
-        for (int ks = 0; ks < 2 * kNPB; ks++) {
-            const uint32_t tr = 16 * ks + 4 * g + (l16 >> 2);
-#pragma unroll
-            for (int c = 0; c < S::CT; c++) {
+        tile_pass<D, false>(
+            tile * kTile, P, qb, m, lsum, o,
+            [&](int s, int b) {
+                return *(const h8 *)&sK[buf][32 * b + l32][16 * s + 8 * g];
+            },
+            [&](int ks, int c) {
+                const uint32_t tr = 16 * ks + 4 * g + (l16 >> 2);
                 const uint32_t tc = 32 * c + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
                 const h4 x = lds_read_tr(&sV[buf][tr][tc]);
                 const h4 y = lds_read_tr(&sV[buf][tr + 8][tc]);
-                const h8 va = h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-                o[c] = mfma(va, pa[ks], o[c]);
-            }
-        }
-        if (tile < tlast) {
+                return h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+            });
+        if (tile < P.tlast) {
             __syncthreads(); /* every wave is done with the other buffer */
             store(buf ^ 1, kr, vr, kz, vz);
             __syncthreads();
         }
     }
+    write_out<D>(A, P, lsum, o);
+}
 
-    /* ---- out = sums / weights, gated ---- */
-    const float lt = lsum + __shfl_xor(lsum, 32, 64);
-    if (!rok)
-        return;
-    const float inv = 1.0f / lt;
-    const size_t obase = ((size_t)rj * A.n_head + rh) * hd;
+/*
+ * The f16 kernel for head sizes 72..128: the next tile goes straight from
+ * HBM (or L2) into LDS with global_load_lds_dwordx4 while this tile is
+ * computed - no staging registers, no LDS stores, one barrier a tile.
+ *
+ * A tile is 128 rows of 256 bytes, unpadded; the 16-byte unit u of row r is
+ * kept in slot u ^ swz(r), swz(r) = rotl4(r mod 16). A load instruction
+ * fills 1 KB (4 rows) contiguously, so lane i fetches the unit that belongs
+ * in its slot. The swizzle keeps both operand reads free of bank conflicts:
+ * a score operand reads one unit of 16 consecutive rows (swz is a bijection
+ * on them), a transposed value read two neighbouring units of 4 consecutive
+ * rows (swz(r) >> 1 differs across the 4, so the 8 slots differ).
+ *
+ * Two buffer pairs, as distinct arrays, and the tile loop unrolled by two:
+ * the compiler then sees that reads of one pair never touch the loads in
+ * flight into the other, and waits for those only at the tile's barrier.
+ */
+__device__ __forceinline__ uint32_t swz(uint32_t r)
+{
+    r &= 15;
+    return ((r << 1) | (r >> 3)) & 15;
+}
+
+template <int D>
+__global__ __launch_bounds__(512) void prefill_dma_kernel(const PrefillArgs A)
+{
+    static_assert(D == 128, "rows of 16 units");
+    constexpr uint32_t RB = D * 2;        /* bytes a row */
+    constexpr uint32_t TB = kTile * RB;   /* bytes a tile */
+    constexpr int CT = D / 32;
+    __shared__ __attribute__((aligned(1024))) char sK0[TB];
+    __shared__ __attribute__((aligned(1024))) char sV0[TB];
+    __shared__ __attribute__((aligned(1024))) char sK1[TB];
+    __shared__ __attribute__((aligned(1024))) char sV1[TB];
+
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t g = lane >> 5, l32 = lane & 31, l16 = lane & 15;
+    const PBlock P = block_of(A);
+    const SeqDesc &sq = *P.sq;
+    const uint32_t hd = A.hd;
+    const bool ring = A.ring != 0;
+    h8 qb[D / 16];
+    load_query<D>(A, P, qb);
+
+    /* loads: instruction j of wave w fills rows 4 (w + 8 j) .. + 3, lane i
+       row 4 (w + 8 j) + i / 16, slot i % 16; columns past hd read column 0
+       (their products meet zero query columns, or are not stored) */
+    const uint32_t drow = 4 * w + (lane >> 4);
+    const uint32_t dunit = (lane & 15) ^ swz(drow);
+    const uint32_t dcol = dunit * 8 < hd ? dunit * 8 : 0;
+    /* held in registers: read through P.sq inside the loop they would be
+       reloaded after every load into LDS, and a pending scalar load makes
+       each LDS operand wait drain the whole queue */
+    const uint16_t *const kg = (const uint16_t *)sq.k, *const vg = (const uint16_t *)sq.v;
+    const uint32_t cap = sq.cap;
+    auto fetch = [&](uint32_t tile, char *dk, char *dv) {
 #pragma unroll
-    for (int c = 0; c < S::CT; c++)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; q4++) {
-            const uint32_t col = 32 * c + 8 * q4 + 4 * g;
-            if (col >= hd)
-                continue;
-            float x[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                x[e] = o[c][4 * q4 + e] * inv;
-                if (A.gate_mode == kGateElem)
-                    x[e] *= 1.0f / (1.0f + expf(-sq.gate[obase + col + e]));
-                else if (A.gate_mode == kGateHead)
-                    x[e] *= 1.0f / (1.0f + expf(-sq.gate[(size_t)rj * A.n_head + rh]));
-            }
-            *(float4 *)(sq.out + obase + col) = float4{x[0], x[1], x[2], x[3]};
+        for (int j = 0; j < (int)(kTile / 32); j++) {
+            const size_t cr = cache_row(P, cap, ring, tile * kTile + drow + 32 * j);
+            const size_t off = cr * hd + dcol;
+            const uint32_t at = (w + 8 * j) * 1024;
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(kg + off),
+                (__attribute__((address_space(3))) void *)(dk + at), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(vg + off),
+                (__attribute__((address_space(3))) void *)(dv + at), 16, 0, 0);
         }
+    };
+    /* operand addresses: the lane's score rows are 32 b + l % 32 (row mod
+       16 = l % 16), its value rows 16 ks + 4 (l / 32) + (l % 16) / 4 and 8
+       further */
+    uint32_t koff[D / 16];
+#pragma unroll
+    for (int s = 0; s < D / 16; s++)
+        koff[s] = l32 * RB + (((2 * s + g) ^ swz(l16)) * 16);
+    const uint32_t vrow = 4 * g + (l16 >> 2);
+    const uint32_t u0 = 2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1);
+    uint32_t vxo[CT], vyo[CT];
+#pragma unroll
+    for (int c = 0; c < CT; c++) {
+        vxo[c] = vrow * RB + (((4 * c + u0) ^ swz(vrow)) * 16) + (l16 & 1) * 8;
+        vyo[c] = (vrow + 8) * RB + (((4 * c + u0) ^ swz(vrow + 8)) * 16) + (l16 & 1) * 8;
+    }
+
+    float m = -INFINITY, lsum = 0.0f;
+    f16x o[CT];
+#pragma unroll
+    for (int c = 0; c < CT; c++)
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            o[c][i] = 0.0f;
+
+    /* tile t from (ck, cv) while t + 1 is loaded into (nk, nv); the
+       scheduling barrier keeps the loads at the top, where they have the
+       whole tile to land */
+    auto step = [&](uint32_t tile, const char *ck, const char *cv, char *nk, char *nv) {
+        if (tile < P.tlast)
+            fetch(tile + 1, nk, nv);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_pass<D, true>(
+            tile * kTile, P, qb, m, lsum, o,
+            [&](int s, int b) { return *(const h8 *)(ck + 32 * b * RB + koff[s]); },
+            [&](int ks, int c) {
+                const char *base = cv + 16 * ks * RB;
+                const h4 x = lds_read_tr((const _Float16 *)(base + vxo[c]));
+                const h4 y = lds_read_tr((const _Float16 *)(base + vyo[c]));
+                return h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+            });
+        if (tile < P.tlast)
+            __syncthreads(); /* the next tile is in; this one is read */
+    };
+
+    fetch(P.tfirst, sK0, sV0);
+    __syncthreads();
+    for (uint32_t tile = P.tfirst;; tile += 2) {
+        step(tile, sK0, sV0, sK1, sV1);
+        if (tile + 1 > P.tlast)
+            break;
+        step(tile + 1, sK1, sV1, sK0, sV0);
+        if (tile + 2 > P.tlast)
+            break;
+    }
+    write_out<D>(A, P, lsum, o);
 }
 
 template <int T, int D>
 hipError_t launch_d(const PrefillArgs &a, hipStream_t s)
 {
-    hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(a.n_wg), dim3(512), 0, s, a);
+    if constexpr (T == kF16 && D == 128)
+        hipLaunchKernelGGL((prefill_dma_kernel<D>), dim3(a.n_wg), dim3(512), 0, s, a);
+    else
+        hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(a.n_wg), dim3(512), 0, s, a);
     return hipGetLastError();
 }
 

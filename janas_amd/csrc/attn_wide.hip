@@ -53,7 +53,8 @@ constexpr int kWWaves = 4;                  /* waves a workgroup */
 constexpr int kWPos = kChunk / kWWaves;     /* 64 positions a wave */
 constexpr int kRound = 16;                  /* positions a round */
 constexpr int kRounds = kWPos / kRound;     /* 4 K rounds, then 4 V rounds */
-constexpr int kWD = 512;                    /* padded head size */
+constexpr int kWD = 512;                    /* largest head size */
+constexpr int kWBuf = 2;                    /* rounds of loads in flight */
 
 __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c)
 {
@@ -72,31 +73,33 @@ __device__ __forceinline__ void split16(h4 raw, h4 &hi, h4 &lo)
     }
 }
 
-template <int T> struct WShape {
+template <int T, int D> struct WShape {
     static_assert(T == kI8 || T == kI16 || T == kF16, "8- and 16-bit caches");
     static constexpr int EB = Elem<T>::bytes;
     static constexpr int KP = Elem<T>::planes;      /* K planes */
     static constexpr int VP = T == kI16 ? 2 : 1;    /* V planes (int8 widened) */
     static constexpr bool SCALED = T == kI8 || T == kI16;
-    static constexpr int RB = kWD * EB;             /* bytes of a padded row */
+    static constexpr int RB = D * EB;               /* bytes of a padded row */
+    static constexpr int VB = D * 2;                /* a V row in LDS (16-bit) */
     static constexpr int UNITS = kRound * RB / 1024; /* 16-byte loads a lane a round */
-    static constexpr int KS = kWD / 32;             /* score k-steps */
-    static constexpr int NT = kWD / 16;             /* output column tiles */
-    static constexpr int QV = kWD / 64;             /* q float4 a lane */
-    static constexpr int QP = kWD + 16;             /* halves a q row in LDS */
-    /* a wave's region: a round's rows (V as 16-bit: 16 KB), later half of
-       its sums ([NT / 2][64] f4, 16 KB) */
-    static constexpr int REGION = 16 * kBlk;
+    static constexpr int KS = D / 32;               /* score k-steps */
+    static constexpr int NT = D / 16;               /* output column tiles */
+    static constexpr int QV = D / 64;               /* q float4 a lane */
+    static constexpr int QP = D + 16;               /* halves a q row in LDS */
+    /* a wave's region: a round's rows (V as 16-bit: 16 VB bytes), later
+       half of its sums ([NT / 2][64] f4, as many bytes) */
+    static constexpr int REGION = kRound * VB / 1024 * kBlk;
 };
 
-template <int T>
+template <int T, int D, int NB>
 __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 {
     using E = Elem<T>;
-    using S = WShape<T>;
+    using S = WShape<T, D>;
     static_assert(S::UNITS * 1024 == kRound * S::RB, "whole kilobytes a round");
-    static_assert(2 * S::UNITS + S::QV + 2 < 63, "the loads fit the wait counter");
-    static_assert(kRound * kWD * 2 <= S::REGION && S::NT / 2 * 64 * 16 <= S::REGION,
+    static_assert(NB * S::UNITS + S::QV + 2 < 63, "the loads fit the wait counter");
+    static_assert(NB >= 1 && NB <= 2 * kRounds, "rounds in flight");
+    static_assert(kRound * S::VB <= S::REGION && S::NT / 2 * 64 * 16 <= S::REGION,
                   "a round of V rows and half the sums fit the region");
     __shared__ __attribute__((aligned(16))) char sW[kWWaves * S::REGION];
     __shared__ __attribute__((aligned(16))) _Float16 sQ[2][kRows][S::QP];
@@ -195,9 +198,10 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
             buf[i] = __builtin_nontemporal_load((const u4 *)(base + off));
         }
     };
-    u4 bufA[S::UNITS], bufB[S::UNITS];
-    load_round(bufA, 0);
-    load_round(bufB, 1);
+    u4 buf[NB][S::UNITS];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+        load_round(buf[b], b);
 
     /* ---- q: scaled by 2^e so that the row's largest |q| lies in
        [2^13, 2^14), split into f16 planes, into LDS ---- */
@@ -251,10 +255,11 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     for (int t = 0; t < S::NT; t++)
         o[t] = f4{0, 0, 0, 0};
 
-    /* step s (a compile-time constant): round s into LDS, round s + 2
+    /* step s (a compile-time constant): round s into LDS, round s + NB
        asked for, round s computed on */
-    auto step = [&](u4 *buf, auto step_no) {
+    auto step = [&](auto step_no) {
         constexpr int s = decltype(step_no)::value;
+        u4 *const b = buf[s % NB];
         /* round s into the region (the wave's reads of the previous round
            are done: LDS serves a wave in order) */
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -265,13 +270,13 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
                 const uint32_t row = byte / S::RB, cb = byte % S::RB;
                 bool back;
                 (void)unit_at(cb, hd, back);
-                const u4 x = unit_fix(buf[i], back);
+                const u4 x = unit_fix(b[i], back);
                 if constexpr (s >= kRounds) {
                     /* values widened to f16 rows of 1 KB */
-                    const h8 a = Elem<kI8>::widen(x.x, x.y);
-                    const h8 b = Elem<kI8>::widen(x.z, x.w);
-                    *(h8 *)(reg + blk_off(row * 1024 + cb * 2)) = a;
-                    *(h8 *)(reg + blk_off(row * 1024 + cb * 2 + 16)) = b;
+                    const h8 lo8 = Elem<kI8>::widen(x.x, x.y);
+                    const h8 hi8 = Elem<kI8>::widen(x.z, x.w);
+                    *(h8 *)(reg + blk_off(row * S::VB + cb * 2)) = lo8;
+                    *(h8 *)(reg + blk_off(row * S::VB + cb * 2 + 16)) = hi8;
                 } else {
                     *(u4 *)(reg + blk_off(byte)) = x;
                 }
@@ -279,11 +284,11 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
         } else {
 #pragma unroll
             for (int i = 0; i < S::UNITS; i++)
-                *(u4 *)(reg + blk_off(i * 1024 + lane * 16)) = buf[i];
+                *(u4 *)(reg + blk_off(i * 1024 + lane * 16)) = b[i];
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if constexpr (s + 2 < 2 * kRounds)
-            load_round(buf, s + 2);
+        if constexpr (s + NB < 2 * kRounds)
+            load_round(b, s + NB);
 
         if constexpr (s < kRounds) {
             /* scores of round s: 4 accumulators (even / odd k-step, high /
@@ -332,7 +337,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
                 for (int t = 0; t < 8; t++) {
                     const uint32_t r1 = 4 * g16 + (l16 >> 2);
                     const uint32_t cc = 16 * (t8 + t) + 4 * (l16 & 3);
-                    const h4 x = lds_read_tr((const _Float16 *)(reg + blk_off(r1 * 1024 + cc * 2)));
+                    const h4 x = lds_read_tr((const _Float16 *)(reg + blk_off(r1 * S::VB + cc * 2)));
                     if constexpr (T == kI16)
                         split16(x, vb[t][0], vb[t][1]);
                     else
@@ -387,14 +392,15 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
             lsum += __shfl_xor(lsum, 32, 64);
         }
     };
-    step(bufA, std::integral_constant<int, 0>());
-    step(bufB, std::integral_constant<int, 1>());
-    step(bufA, std::integral_constant<int, 2>());
-    step(bufB, std::integral_constant<int, 3>());
-    step(bufA, std::integral_constant<int, 4>());
-    step(bufB, std::integral_constant<int, 5>());
-    step(bufA, std::integral_constant<int, 6>());
-    step(bufB, std::integral_constant<int, 7>());
+    static_assert(2 * kRounds == 8, "eight steps");
+    step(std::integral_constant<int, 0>());
+    step(std::integral_constant<int, 1>());
+    step(std::integral_constant<int, 2>());
+    step(std::integral_constant<int, 3>());
+    step(std::integral_constant<int, 4>());
+    step(std::integral_constant<int, 5>());
+    step(std::integral_constant<int, 6>());
+    step(std::integral_constant<int, 7>());
 
     /* ---- the 4 waves combined: chunk max M, wave w's sums weighted by
        e^(m_w - M) (and back to 2^0), then summed over the waves in a fixed
@@ -458,6 +464,13 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     }
 }
 
+template <int T, int D, int NB>
+hipError_t launch_w(const SplitArgs &a, hipStream_t s)
+{
+    hipLaunchKernelGGL((wide_kernel<T, D, NB>), dim3(a.n_wg), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_wide(int kv, const SplitArgs &a, hipStream_t s)
@@ -466,18 +479,13 @@ hipError_t launch_wide(int kv, const SplitArgs &a, hipStream_t s)
         return hipErrorInvalidValue;
     switch (kv) {
     case kI8:
-        hipLaunchKernelGGL(wide_kernel<kI8>, dim3(a.n_wg), dim3(256), 0, s, a);
-        break;
+        return launch_w<kI8, kWD, kWBuf>(a, s);
     case kI16:
-        hipLaunchKernelGGL(wide_kernel<kI16>, dim3(a.n_wg), dim3(256), 0, s, a);
-        break;
+        return launch_w<kI16, kWD, kWBuf>(a, s);
     case kF16:
-        hipLaunchKernelGGL(wide_kernel<kF16>, dim3(a.n_wg), dim3(256), 0, s, a);
-        break;
-    default:
-        return hipErrorInvalidValue;
+        return launch_w<kF16, kWD, kWBuf>(a, s);
     }
-    return hipGetLastError();
+    return hipErrorInvalidValue;
 }
 
 }  // namespace janas
