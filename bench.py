@@ -1,7 +1,7 @@
 """Benchmark of the KV-cache attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                    [--only decode|prefill|copy]
+                    [--only decode|prefill|wide|copy]
 
 Headline (BASELINE.json metric): decode attention KV GB/s at 32k context on
 BASELINE config 4 - 16 query / 2 KV heads, head_dim 256, 32,768 positions,
@@ -11,7 +11,10 @@ cache (the split kernel and the merge). Inputs are synthetic N(0, 1), drawn
 from a fixed seed, resident in HBM before timing starts. The prefill figure
 rides along in the same line under "prefill": one causal call over an
 8,192-token prompt, its algorithmic flops (4 x head_dim per visible
-(token, head, position)) over the launch time.
+(token, head, position)) over the launch time. Under "wide": Gemma 4's
+head size - a decode step at 32k over an int16 cache with head_dim 512
+(16 / 2 heads, the reference test's score scale 0.02), the wide kernel's
+KV bytes (and scales) over its launch time.
 
 Prints one JSON line. ``roofline`` is the split kernel's: its algorithmic
 bytes (every K/V element of the visible positions once) over its average
@@ -52,6 +55,18 @@ def decode_workload():
                 v=normal(rng, (kvh, L, hd), np.float16),
                 q=normal(rng, (1, h, hd), np.float32),
                 g=normal(rng, (1, h, hd), np.float32))
+
+
+def wide_workload():
+    """head_dim 512 over an int16 cache (Gemma 4's full-attention layers):
+    keys and values uniform int16, scales U(0.001, 0.02) / 258 as the
+    reference's test draws them (test_attention.c:270-279)."""
+    h, kvh, hd, L = 16, 2, 512, 32768
+    rng = np.random.default_rng(SEED + 4)
+    ints = lambda: rng.integers(-32767, 32768, (kvh, L, hd), dtype=np.int16)
+    scl = lambda: (rng.uniform(0.001, 0.02, (kvh, L)) / 258.0).astype(np.float32)
+    return dict(h=h, kvh=kvh, hd=hd, L=L, scale=0.02, k=ints(), v=ints(),
+                ks=scl(), vs=scl(), q=normal(rng, (1, h, hd), np.float32))
 
 
 def prefill_workload():
@@ -132,19 +147,22 @@ def cpu_prefill_baseline(w, block=64):
 NCOPY = 6  # 6 caches of 67 MB: more than the 256 MB infinity cache
 
 
-def bench_decode(torch, jm, w, steps, warmup):
+def bench_decode(torch, jm, w, steps, warmup, kv=None, ncopy=NCOPY):
     """Decode steps (split + merge kernels) launched back to back on one
-    stream, each over the next of NCOPY copies of the cache - a real decode
+    stream, each over the next of ncopy copies of the cache - a real decode
     reads another layer's cache each call, so none stays in the 256 MB
     infinity cache. Then each kernel's average launch time: a batch of its
     launches alone, bracketed by HIP events on the same stream."""
     dev = torch.device("cuda:0")
+    kv = jm.KV_F16 if kv is None else kv
     k0 = torch.from_numpy(w["k"]).to(dev)
     v0 = torch.from_numpy(w["v"]).to(dev)
-    ks = [k0] + [k0.clone() for _ in range(NCOPY - 1)]
-    vs = [v0] + [v0.clone() for _ in range(NCOPY - 1)]
+    ks = [k0] + [k0.clone() for _ in range(ncopy - 1)]
+    vs = [v0] + [v0.clone() for _ in range(ncopy - 1)]
+    kz = torch.from_numpy(w["ks"]).to(dev) if "ks" in w else None
+    vz = torch.from_numpy(w["vs"]).to(dev) if "vs" in w else None
     q = torch.from_numpy(w["q"]).to(dev)
-    g = torch.from_numpy(w["g"]).to(dev)
+    g = torch.from_numpy(w["g"]).to(dev) if "g" in w else None
     out = torch.empty_like(q)
     a = jm.Attention(w["h"], w["kvh"], w["hd"], w["L"])
     a.set_scale(w["scale"])
@@ -154,23 +172,24 @@ def bench_decode(torch, jm, w, steps, warmup):
     stream = torch.cuda.Stream()
 
     def calls(path):
-        return [a.prepare(jm.KV_F16, [dict(k=ks[i], v=vs[i], q=q, out=out,
-                                           gate=g, cap=w["L"], n=1,
-                                           pos0=w["L"] - 1)],
-                          gate_mode=jm.GATE_ELEM, stream=stream.cuda_stream,
-                          path=path) for i in range(NCOPY)]
+        return [a.prepare(kv, [dict(k=ks[i], v=vs[i], ks=kz, vs=vz, q=q,
+                                    out=out, gate=g, cap=w["L"], n=1,
+                                    pos0=w["L"] - 1)],
+                          gate_mode=jm.GATE_ELEM if g is not None else
+                          jm.GATE_NONE, stream=stream.cuda_stream,
+                          path=path) for i in range(ncopy)]
 
     def timed(fns, n):
         assert stream.cuda_stream != 0
         for i in range(warmup):
-            fns[i % NCOPY]()
+            fns[i % ncopy]()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(
             enable_timing=True)
         t0 = time.perf_counter()
         e0.record(stream)
         for i in range(n):
-            fns[i % NCOPY]()
+            fns[i % ncopy]()
         e1.record(stream)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n, time.perf_counter() - t0
@@ -222,6 +241,32 @@ def bench_copy(torch, steps):
                       "copy_bytes_written": dst.numel() * 4}), flush=True)
 
 
+def wide_leg(torch, jm, steps, warmup):
+    """The head_dim 512 int16 decode (wide kernel + merge), 3 cache copies
+    of 134 MB so none stays in the infinity cache."""
+    w = wide_workload()
+    ms, _, split_ms, merge_ms = bench_decode(torch, jm, w, steps, warmup,
+                                             kv=jm.KV_I16, ncopy=3)
+    kv_bytes = 2 * w["kvh"] * w["L"] * w["hd"] * 2 + 2 * w["kvh"] * w["L"] * 4
+    achieved = kv_bytes / (split_ms * 1e-3) / 1e9
+    return {
+        "metric": "hd-512 int16 decode attn KV GB/s @32k",
+        "value": round(kv_bytes / (ms * 1e-3) / 1e9, 2), "unit": "GB/s",
+        "ms": round(ms, 5),
+        "config": {"workload": "decode, 16 Q / 2 KV heads, head_dim 512, "
+                               "32768 positions, int16 K/V with per-row "
+                               "scales, f32 q, score scale 0.02",
+                   "kv_bytes": kv_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles("wide_kernel_hd512"),
+                     "kernel": "wide_kernel<i16, 512, 2>",
+                     "kernel_us": round(split_ms * 1e3, 3),
+                     "merge_us": round(merge_ms * 1e3, 3)},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -229,7 +274,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=("decode", "prefill", "copy"),
+    ap.add_argument("--only", choices=("decode", "prefill", "wide", "copy"),
                     help="run one leg alone (profiling)")
     ap.add_argument("--prefill-steps", type=int, default=20)
     args = ap.parse_args()
@@ -250,6 +295,10 @@ def main():
         wp = prefill_workload()
         pms = bench_prefill(torch, jm, wp, args.prefill_steps, 3)
         print(json.dumps({"prefill_ms": pms}), flush=True)
+        return
+    if args.only == "wide":
+        print(json.dumps(wide_leg(torch, jm, args.steps, args.warmup)),
+              flush=True)
         return
     w = decode_workload()
     ms, wall, split_ms, merge_ms = bench_decode(torch, jm, w, args.steps,
@@ -301,9 +350,11 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tf, 2),
                      "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
-                     "traffic": traffic_from_profiles("prefill_kernel_8k"),
+                     "traffic": traffic_from_profiles("prefill_dma_kernel_8k"),
                      "kernel": "prefill_dma_kernel<128>"},
     }
+    line["wide"] = wide_leg(torch, jm, max(1, args.steps // 4),
+                            min(args.warmup, 20))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_decode_baseline(w)
         line["prefill"]["cpu_baseline"] = cpu_prefill_baseline(wp)
