@@ -223,8 +223,13 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
         uint32_t m = std::min(kMaxSeqs, n_seqs - s0);
         SplitArgs args;
         memset(&args, 0, sizeof args);
-        uint64_t rows = 0;
-        uint32_t wg = 0, mg = 0, nd = (a->hd + 31) / 32; /* merge: 32 columns a workgroup */
+        uint64_t rows = 0, pairs = 0;
+        for (uint32_t i = 0; i < m; i++)
+            pairs += (uint64_t)seqs[s0 + i].n * a->n_head;
+        args.merge_cols = merge_cols(pairs, a->hd);
+        args.once = 1;
+        uint32_t wg = 0, mg = 0;
+        const uint32_t nd = (a->hd + args.merge_cols - 1) / args.merge_cols;
         for (uint32_t i = 0; i < m; i++) {
             SeqDesc &d = args.seq[i];
             int rc = describe(a, kv, seqs[s0 + i], d);
@@ -233,6 +238,7 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
             d.wg0 = wg;
             d.mg0 = mg;
             d.part0 = rows;
+            args.once &= d.rtiles == 1;
             uint64_t nwg = (uint64_t)a->n_kv * d.span * d.rtiles;
             uint64_t nmg = (uint64_t)d.n * a->n_head * nd;
             if (wg + nwg > 0x7FFFFFFFu || mg + nmg > 0x7FFFFFFFu)

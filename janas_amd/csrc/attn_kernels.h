@@ -18,6 +18,9 @@ namespace janas {
 constexpr uint32_t kChunk = 256;
 /* sequences one launch takes (by value in its arguments) */
 constexpr uint32_t kMaxSeqs = 16;
+/* merge workgroups a launch keeps at least when it takes 128 columns a
+   workgroup (merge_cols) */
+constexpr uint64_t kMergeFill = 512;
 
 enum KvType : int { kI8 = 0, kI16 = 1, kF16 = 2, kF32 = 3 };
 enum GateMode : int { kGateNone = 0, kGateElem = 1, kGateHead = 2 };
@@ -45,6 +48,8 @@ struct SplitArgs {
     float *part_ml;        /* [rows][2]: largest score, sum of weights */
     float *part_acc;       /* [rows][hd]: weighted values */
     uint32_t n_seqs, n_wg;
+    uint32_t once;         /* every sequence one row tile: K/V read once */
+    uint32_t merge_cols;   /* 32 or 128 columns a merge workgroup */
     uint32_t n_head, n_kv, group, hd, window;
     float scale;
     int ring;
@@ -99,6 +104,8 @@ struct Q8kArgs {
 /* Launchers (attn_split.hip). Return hipSuccess or the launch's error. */
 hipError_t launch_split(int kv, const SplitArgs &a, hipStream_t s);
 hipError_t launch_merge(const SplitArgs &a, uint32_t n_wg, hipStream_t s);
+/* columns a merge workgroup takes for a launch of pairs (token, head). */
+uint32_t merge_cols(uint64_t pairs, uint32_t hd);
 /* 1 when the split kernel has an instance for this element type and
    padded head size. */
 int split_supported(int kv, uint32_t hd);

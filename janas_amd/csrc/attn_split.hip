@@ -22,7 +22,7 @@
  *                  in LDS in a fixed order into the chunk's exact partial.
  *                  Workgroups are renumbered so each XCD takes a contiguous
  *                  range (neighbouring chunks share an L2).
- *   merge kernel   one workgroup per (token, query head, 32 columns): the
+ *   merge kernel   one workgroup per (token, query head, 32 or 128 columns): the
  *                  ordered merge of the chunk partials (8 groups of chunks in
  *                  parallel, each in batches of 16, combined in a fixed
  *                  tree), the output gate sigmoid(g) * o (model_attn.c:
@@ -73,8 +73,11 @@ namespace {
  * softmax is one shot over its 32 positions; the 8 waves' (max, sum,
  * values) are combined at the end. No load goes straight to LDS: with
  * those in flight the compiler makes every barrier and every use of a
- * register load wait for all of them. K and V are read once, so their
- * loads are nontemporal (15.7 against 16.6 us on the 32k decode).
+ * register load wait for all of them. In a decode K and V are read once,
+ * so their loads are nontemporal (15.7 against 16.6 us on the 32k decode);
+ * the row tiles of a block of tokens read a chunk each, and plain loads
+ * keep it in L2 for them (the NT instance is the decode one: a branch
+ * between the two in one kernel cost the decode 6 %).
  */
 constexpr int kWaves = 8;
 constexpr int kWavePos = kChunk / kWaves; /* 32 */
@@ -96,7 +99,7 @@ template <int T, int D> struct Shape {
     static constexpr int REGION = RROWS > RSUM ? RROWS : RSUM;
 };
 
-template <int T, int D>
+template <int T, int D, bool NT>
 __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
 {
     using E = Elem<T>;
@@ -191,9 +194,17 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
         }
         off[i] = (crow + ((p < plast ? p : plast) - t0)) * (hd * S::EB) + at;
     }
+    /* NT: every chunk is read by one row tile (decode), once: nontemporal;
+       one that several row tiles read (blocks of tokens) should stay in L2 */
+    if constexpr (NT) {
 #pragma unroll
-    for (int i = 0; i < S::UNITS; i++)
-        kraw[i] = __builtin_nontemporal_load((const u4 *)((const char *)sq.k + off[i]));
+        for (int i = 0; i < S::UNITS; i++)
+            kraw[i] = __builtin_nontemporal_load((const u4 *)((const char *)sq.k + off[i]));
+    } else {
+#pragma unroll
+        for (int i = 0; i < S::UNITS; i++)
+            kraw[i] = *(const u4 *)((const char *)sq.k + off[i]);
+    }
     /* the scales of the lane's positions 16 mt + 4 g16 + i */
     float ks8[8], vs8[8];
 #pragma unroll
@@ -256,9 +267,15 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
         *(u4 *)(reg + blk_off(i * 1024 + lane * 16)) =
             S::EB == 1 ? unit_fix(kraw[i], back[i]) : kraw[i];
     /* V once the wave's K is in */
+    if constexpr (NT) {
 #pragma unroll
-    for (int i = 0; i < S::UNITS; i++)
-        vraw[i] = __builtin_nontemporal_load((const u4 *)((const char *)sq.v + off[i]));
+        for (int i = 0; i < S::UNITS; i++)
+            vraw[i] = __builtin_nontemporal_load((const u4 *)((const char *)sq.v + off[i]));
+    } else {
+#pragma unroll
+        for (int i = 0; i < S::UNITS; i++)
+            vraw[i] = *(const u4 *)((const char *)sq.v + off[i]);
+    }
     f4 sacc[2];
     {
         f4 sa[2][2] = {{f4{0, 0, 0, 0}, f4{0, 0, 0, 0}}, {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}}};
@@ -459,8 +476,8 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
 }
 
 /*
- * Merge of the chunk partials of (token j, query head h), 32 columns a
- * workgroup (attention.c:870-910). Group g of 8 (32 lanes each, a lane a
+ * Merge of the chunk partials of (token j, query head h), 32 or 128 columns
+ * a workgroup (attention.c:870-910). Group g of 8 (32 lanes each, a lane a
  * column) takes chunks g, g + 8, ... of the token's range, 16 at a time in
  * one batch of loads: their largest score M_g, then sum_c e^(m_c - M_g) l_c
  * and acc_c in chunk order. The groups are combined with weights
@@ -469,20 +486,35 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
  * same way in any block. The gate sigmoid(g) * o is applied on the way out.
  */
 constexpr int kMergeGroups = 8;
-constexpr int kMergeCols = 32;
+constexpr int kMergeLanes = 32;            /* lanes a group */
 constexpr int kMergeBatch = 16;
 
+/* the 4 columns of a float4, one by one */
+__device__ __forceinline__ float &f4e(float4 &v, int e)
+{
+    return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+}
+
+/*
+ * CPL columns a lane (1 or 4: 32 or 128 columns a workgroup). Each column's
+ * arithmetic is the same in both, so a token's output does not depend on
+ * the instance its call takes; 4 when a launch has (token, head) pairs
+ * enough to fill the GPU with 4 times fewer workgroups (blocks of tokens),
+ * 1 when it has few (a decode spreads its loads over more CUs).
+ */
+template <int CPL>
 __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 {
+    constexpr uint32_t kCols = kMergeLanes * CPL;
     __shared__ float sM[kMergeGroups], sL[kMergeGroups];
-    __shared__ float sAcc[kMergeGroups][kMergeCols];
+    __shared__ float4 sAcc[kMergeGroups][kMergeLanes];
     const uint32_t id = blockIdx.x, tid = threadIdx.x;
-    const uint32_t g = tid / kMergeCols, cl = tid % kMergeCols;
+    const uint32_t g = tid / kMergeLanes, cl = tid % kMergeLanes;
     uint32_t si = 0;
     while (si + 1 < A.n_seqs && A.seq[si + 1].mg0 <= id)
         si++;
     const SeqDesc &sq = A.seq[si];
-    const uint32_t hd = A.hd, G = A.group, nd = (hd + kMergeCols - 1) / kMergeCols;
+    const uint32_t hd = A.hd, G = A.group, nd = (hd + kCols - 1) / kCols;
     const uint32_t local = id - sq.mg0, db = local % nd;
     const uint32_t h = (local / nd) % A.n_head, j = local / nd / A.n_head;
     const uint32_t kvh = h / G, r = j * G + h % G, R = sq.n * G;
@@ -491,19 +523,26 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     const uint32_t clo = lo / kChunk, nc = hi / kChunk - clo + 1;
     /* partial row of chunk clo + i */
     const uint64_t base = sq.part0 + ((uint64_t)kvh * sq.span + (clo - sq.c0)) * R + r;
-    const uint32_t col = db * kMergeCols + cl;
+    /* the lane's columns col .. col + CPL - 1 (hd is a multiple of 8: all
+       are inside the row or none is) */
+    const uint32_t col = db * kCols + CPL * cl;
     const bool colok = col < hd;
-    float mg = -INFINITY, lg = 0.0f, ag = 0.0f;
+    float mg = -INFINITY, lg = 0.0f;
+    float4 ag = {0.0f, 0.0f, 0.0f, 0.0f};
     for (uint32_t i0 = g; i0 < nc; i0 += kMergeGroups * kMergeBatch) {
         float2 ml[kMergeBatch];
-        float v[kMergeBatch];
+        float4 v[kMergeBatch];
         /* branch-free: chunks past the range read the last one, weight 0 */
 #pragma unroll
         for (int b = 0; b < kMergeBatch; b++) {
             const uint32_t i = i0 + kMergeGroups * b < nc ? i0 + kMergeGroups * b : nc - 1;
             const uint64_t pr = base + (uint64_t)i * R;
             ml[b] = *(const float2 *)(A.part_ml + pr * 2);
-            v[b] = A.part_acc[pr * hd + (colok ? col : 0)];
+            const float *src = A.part_acc + pr * hd + (colok ? col : 0);
+            if constexpr (CPL == 4)
+                v[b] = *(const float4 *)src;
+            else
+                v[b].x = *src;
         }
         float mb = mg;
 #pragma unroll
@@ -513,12 +552,16 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
         /* the batch's sums, against the group's new largest score */
         const float f = mg == -INFINITY ? 0.0f : expf(mg - mb);
         lg *= f;
-        ag *= f;
+#pragma unroll
+        for (int e = 0; e < CPL; e++)
+            f4e(ag, e) *= f;
 #pragma unroll
         for (int b = 0; b < kMergeBatch; b++) {
             const float wgt = i0 + kMergeGroups * b < nc ? expf(ml[b].x - mb) : 0.0f;
             lg += wgt * ml[b].y;
-            ag = fmaf(wgt, v[b], ag);
+#pragma unroll
+            for (int e = 0; e < CPL; e++)
+                f4e(ag, e) = fmaf(wgt, f4e(v[b], e), f4e(ag, e));
         }
         mg = mb;
     }
@@ -534,28 +577,56 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 #pragma unroll
     for (int k = 0; k < kMergeGroups; k++)
         mx = fmaxf(mx, sM[k]);
-    float wl[kMergeGroups], wa[kMergeGroups];
+    float wl[kMergeGroups];
+    float4 wa[kMergeGroups];
 #pragma unroll
     for (int k = 0; k < kMergeGroups; k++) {
         const float wk = sM[k] == -INFINITY ? 0.0f : expf(sM[k] - mx);
+        float4 a = sAcc[k][cl];
         wl[k] = wk * sL[k];
-        wa[k] = wk * sAcc[k][cl];
+#pragma unroll
+        for (int e = 0; e < CPL; e++)
+            f4e(wa[k], e) = wk * f4e(a, e);
     }
     const float sum = ((wl[0] + wl[1]) + (wl[2] + wl[3])) + ((wl[4] + wl[5]) + (wl[6] + wl[7]));
-    float o = (((wa[0] + wa[1]) + (wa[2] + wa[3])) + ((wa[4] + wa[5]) + (wa[6] + wa[7]))) *
-              (1.0f / sum);
+    const float inv = 1.0f / sum;
     const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
-    if (A.gate_mode == kGateElem)
-        o *= 1.0f / (1.0f + expf(-sq.gate[oi]));
-    else if (A.gate_mode == kGateHead)
-        o *= 1.0f / (1.0f + expf(-sq.gate[(size_t)j * A.n_head + h]));
-    sq.out[oi] = o;
+    float4 gv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (A.gate_mode == kGateElem) {
+        if constexpr (CPL == 4)
+            gv = *(const float4 *)(sq.gate + oi);
+        else
+            gv.x = sq.gate[oi];
+    }
+    const float gh = A.gate_mode == kGateHead
+                         ? sq.gate[(size_t)j * A.n_head + h] : 0.0f;
+    float4 o;
+#pragma unroll
+    for (int e = 0; e < CPL; e++) {
+        float x[kMergeGroups];
+#pragma unroll
+        for (int k = 0; k < kMergeGroups; k++)
+            x[k] = f4e(wa[k], e);
+        float y = (((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]))) * inv;
+        if (A.gate_mode == kGateElem)
+            y *= 1.0f / (1.0f + expf(-f4e(gv, e)));
+        else if (A.gate_mode == kGateHead)
+            y *= 1.0f / (1.0f + expf(-gh));
+        f4e(o, e) = y;
+    }
+    if constexpr (CPL == 4)
+        *(float4 *)(sq.out + oi) = o;
+    else
+        sq.out[oi] = o.x;
 }
 
 template <int T, int D>
 hipError_t launch_t(const SplitArgs &a, hipStream_t s)
 {
-    hipLaunchKernelGGL((split_kernel<T, D>), dim3(a.n_wg), dim3(512), 0, s, a);
+    if (a.once)
+        hipLaunchKernelGGL((split_kernel<T, D, true>), dim3(a.n_wg), dim3(512), 0, s, a);
+    else
+        hipLaunchKernelGGL((split_kernel<T, D, false>), dim3(a.n_wg), dim3(512), 0, s, a);
     return hipGetLastError();
 }
 
@@ -599,9 +670,20 @@ hipError_t launch_split(int kv, const SplitArgs &a, hipStream_t s)
     return hipErrorInvalidValue;
 }
 
+uint32_t merge_cols(uint64_t pairs, uint32_t hd)
+{
+    /* 128 columns a workgroup when that still leaves kMergeFill of them */
+    return pairs * ((hd + 127) / 128) >= kMergeFill ? 128 : 32;
+}
+
 hipError_t launch_merge(const SplitArgs &a, uint32_t n_wg, hipStream_t s)
 {
-    hipLaunchKernelGGL(merge_kernel, dim3(n_wg), dim3(256), 0, s, a);
+    if (a.merge_cols == 128)
+        hipLaunchKernelGGL(merge_kernel<4>, dim3(n_wg), dim3(256), 0, s, a);
+    else if (a.merge_cols == 32)
+        hipLaunchKernelGGL(merge_kernel<1>, dim3(n_wg), dim3(256), 0, s, a);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

@@ -229,3 +229,118 @@ def test_int8_rows_of_8_mod_16_bytes(hd, gpu):
     err = abs_err(d["out"].cpu().numpy(), ref)
     print(f"int8 hd {hd}: max abs err {err:.2e}")
     assert err <= TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+
+
+def block_case(kv, n_kv=8, h=32, hd=128, L=4096, n=64, seed=8100):
+    """A 64-token block at the cache's end over 8 KV heads and 16 chunks:
+    16 row tiles read each chunk (plain loads, kept in L2) and the merge
+    takes 128 columns a workgroup."""
+    from cases import uniform
+    cells, rows = n_kv * L * hd, n_kv * L
+    if kv == KV_F16:
+        k = normal_cache(seed + 1, cells).astype(np.float16)
+        v = normal_cache(seed + 2, cells).astype(np.float16)
+        ks = vs = None
+    else:
+        lim = 127 if kv == KV_I8 else 32767
+        dt = np.int8 if kv == KV_I8 else np.int16
+        k = uniform(seed + 1, cells, -lim, lim).astype(np.int32).astype(dt)
+        v = uniform(seed + 2, cells, -lim, lim).astype(np.int32).astype(dt)
+        div = np.float32(1.0 if kv == KV_I8 else 258.0)
+        ks = (uniform(seed + 3, rows, 0.001, 0.02) / div).reshape(n_kv, L)
+        vs = (uniform(seed + 4, rows, 0.001, 0.02) / div).reshape(n_kv, L)
+    q = uniform(seed + 5, n * h * hd, -3, 3).reshape(n, h, hd)
+    return dict(k=k.reshape(n_kv, L, hd), v=v.reshape(n_kv, L, hd), ks=ks,
+                vs=vs, q=q, n_kv=n_kv, h=h, hd=hd, L=L, n=n)
+
+
+def normal_cache(seed, count):
+    from cases import normal
+    return normal(seed, count)
+
+
+def run_block(c, kv, gpu, pos0, window=0, last=None, per_token=False):
+    d = dict(k=to_dev(c["k"], gpu), v=to_dev(c["v"], gpu),
+             q=to_dev(c["q"], gpu), cap=c["L"], n=c["n"], pos0=pos0)
+    if c["ks"] is not None:
+        d["ks"], d["vs"] = to_dev(c["ks"], gpu), to_dev(c["vs"], gpu)
+    d["out"] = torch.zeros(d["q"].shape, dtype=torch.float32, device=gpu)
+    with Attention(c["h"], c["n_kv"], c["hd"], c["L"]) as a:
+        if window:
+            a.set_window(window)
+        if not per_token:
+            if last is not None:
+                d["last"] = to_dev(last, gpu)
+                d["last_max"] = int(last.max())
+            a.run_dev(kv, [d], path="split")
+        else:
+            for j in range(c["n"]):
+                dj = dict(d, q=d["q"][j:j + 1], out=d["out"][j:j + 1], n=1,
+                          pos0=pos0 + j)
+                if last is not None:
+                    dj["last"] = to_dev(last[j:j + 1], gpu)
+                    dj["last_max"] = int(last[j])
+                a.run_dev(kv, [dj], path="split")
+        torch.cuda.synchronize()
+    return d["out"].cpu().numpy()
+
+
+@pytest.mark.parametrize("kv", [KV_F16, KV_I8, KV_I16])
+def test_large_block_equals_tokens(kv, gpu):
+    """A 64-token block over a 4096-position cache equals 64 one-token calls
+    bit for bit (their chunks are loaded nontemporally, the block's are
+    not), and the restatement within the bar."""
+    c = block_case(kv)
+    pos0 = c["L"] - c["n"]
+    blk = run_block(c, kv, gpu, pos0)
+    one = run_block(c, kv, gpu, pos0, per_token=True)
+    assert np.array_equal(blk.view(np.int32), one.view(np.int32))
+    ref = orc.run(c["q"], c["k"], c["v"], c["ks"], c["vs"], n_head=c["h"],
+                  n_kv=c["n_kv"], hd=c["hd"], pos0=pos0, kv=kv, threads=16)
+    err = abs_err(blk, ref)
+    bar = TOL_F16_ABS if kv == KV_F16 else TOL_FLOAT_ABS * max(
+        1.0, float(np.abs(ref).max()))
+    print(f"kv {kv}: large block max abs err {err:.2e} (bar {bar:.1e})")
+    assert err <= bar
+
+
+def test_large_block_window_and_last(gpu):
+    """Row tiles of the block see different chunks: a window of 700 and a
+    span that sees past itself."""
+    c = block_case(KV_I8, seed=8200)
+    pos0 = c["L"] - c["n"] - 500
+    p = pos0 + np.arange(c["n"])
+    last = np.where((p >= pos0 + 10) & (p < pos0 + 30), pos0 + 29, p).astype(
+        np.uint32)
+    blk = run_block(c, KV_I8, gpu, pos0, window=700, last=last)
+    one = run_block(c, KV_I8, gpu, pos0, window=700, last=last, per_token=True)
+    assert np.array_equal(blk.view(np.int32), one.view(np.int32))
+    ref = orc.run(c["q"], c["k"], c["v"], c["ks"], c["vs"], n_head=c["h"],
+                  n_kv=c["n_kv"], hd=c["hd"], pos0=pos0, kv=KV_I8, window=700,
+                  last=last, threads=16)
+    err = abs_err(blk, ref)
+    print(f"large block, window + last: max abs err {err:.2e}")
+    assert err <= TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+
+
+def test_large_block_ragged_sequences(gpu):
+    """Three sequences in one launch (64, 37 and 1 tokens): each equals its
+    own one-token calls bit for bit."""
+    cs = [block_case(KV_F16, seed=8300 + i) for i in range(3)]
+    ns, pos = [64, 37, 1], [4032, 3000, 4095]
+    seqs = []
+    for c, n, p0 in zip(cs, ns, pos):
+        d = dict(k=to_dev(c["k"], gpu), v=to_dev(c["v"], gpu),
+                 q=to_dev(c["q"][:n], gpu), cap=c["L"], n=n, pos0=p0)
+        d["out"] = torch.zeros(d["q"].shape, dtype=torch.float32, device=gpu)
+        seqs.append(d)
+    with Attention(32, 8, 128, 4096) as a:
+        a.run_dev(KV_F16, seqs, path="split")
+        torch.cuda.synchronize()
+        for d, n, p0 in zip(seqs, ns, pos):
+            one = torch.zeros_like(d["out"])
+            for j in range(n):
+                a.run_dev(KV_F16, [dict(d, q=d["q"][j:j + 1], out=one[j:j + 1],
+                                        n=1, pos0=p0 + j)], path="split")
+            torch.cuda.synchronize()
+            assert torch.equal(d["out"].view(torch.int32), one.view(torch.int32))
