@@ -42,9 +42,10 @@
  *                   LDS); lane l holds row l % 16 at positions 4 (l / 16) + i
  *                   of each tile - already the A layout of the value product.
  *   O   = P . V     the weights stay in registers as A operands; V is read
- *                   back transposed with ds_read_b64_tr_b16 (16-bit types)
- *                   or gathered (int8, f32 planes); every wave sums all
- *                   value columns over its positions.
+ *                   back transposed with ds_read_b64_tr_b16 (16-bit types,
+ *                   and int8 rows widened to f16 as they are staged) or
+ *                   gathered (f32 planes); every wave sums all value
+ *                   columns over its positions.
  */
 #include <math.h>
 #include <stdint.h>
@@ -93,10 +94,12 @@ template <int T, int D> struct Shape {
     static constexpr int NT = D / 16;               /* output column tiles */
     static constexpr int QV = D / 128 > 0 ? D / 128 : 1; /* q float4 a lane */
     static constexpr int QP = D + 16;               /* halves a q row in LDS */
-    /* a wave's region: its rows, later its sums ([NT][64] f4) */
-    static constexpr int RROWS = UNITS * kBlk;
+    /* a wave's region: its rows (int8 values widened to f16: twice the
+       bytes), later its sums ([NT][64] f4) */
+    static constexpr int RROWS = (T == kI8 ? 2 : 1) * UNITS * kBlk;
     static constexpr int RSUM = NT * 64 * 16;
     static constexpr int REGION = RROWS > RSUM ? RROWS : RSUM;
+    static constexpr int VRB = T == kI8 ? 2 * RB : RB; /* bytes of a V row in LDS */
 };
 
 template <int T, int D, bool NT>
@@ -368,10 +371,23 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
     /* ---- V into the same region (the wave's reads of K are done: LDS
        serves a wave in order), then the values ---- */
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if constexpr (T == kI8) {
+        /* int8 values widened to f16 rows (exact), read back transposed
+           like the 16-bit types */
 #pragma unroll
-    for (int i = 0; i < S::UNITS; i++)
-        *(u4 *)(reg + blk_off(i * 1024 + lane * 16)) =
-            S::EB == 1 ? unit_fix(vraw[i], back[i]) : vraw[i];
+        for (int i = 0; i < S::UNITS; i++) {
+            const uint32_t byte = i * 1024 + lane * 16;
+            const uint32_t row = byte / S::RB, cb = byte % S::RB;
+            const u4 x = unit_fix(vraw[i], back[i]);
+            *(h8 *)(reg + blk_off(row * S::VRB + cb * 2)) = Elem<kI8>::widen(x.x, x.y);
+            *(h8 *)(reg + blk_off(row * S::VRB + cb * 2 + 16)) = Elem<kI8>::widen(x.z, x.w);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < S::UNITS; i++)
+            *(u4 *)(reg + blk_off(i * 1024 + lane * 16)) =
+                S::EB == 1 ? unit_fix(vraw[i], back[i]) : vraw[i];
+    }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     f4 o[S::NT];
 #pragma unroll
@@ -381,31 +397,27 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
         h8 vbp[S::NT][P];
 #pragma unroll
         for (int t = 0; t < S::NT; t++) {
-            if constexpr (S::EB == 2) {
+            if constexpr (S::EB == 2 || T == kI8) {
                 const uint32_t r1 = 4 * g16 + (l16 >> 2);
                 const uint32_t cc = 16 * t + 4 * (l16 & 3);
-                const h4 x = lds_read_tr((const _Float16 *)(reg + blk_off(r1 * S::RB + cc * 2)));
-                const h4 y = lds_read_tr((const _Float16 *)(reg + blk_off((r1 + 16) * S::RB + cc * 2)));
+                const h4 x = lds_read_tr((const _Float16 *)(reg + blk_off(r1 * S::VRB + cc * 2)));
+                const h4 y = lds_read_tr((const _Float16 *)(reg + blk_off((r1 + 16) * S::VRB + cc * 2)));
                 const h8 xy = h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-                if constexpr (T == kF16)
+                if constexpr (T == kF16 || T == kI8)
                     vbp[t][0] = xy;
                 else
                     Elem<kI16>::split(__builtin_bit_cast(uint4, xy), vbp[t][0], vbp[t][1]);
             } else {
-                /* int8 and f32: the 8 positions of one column, one by one */
+                /* f32: the 8 positions of one column, one by one */
                 const uint32_t cc = 16 * t + l16;
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const uint32_t rv = 16 * (e / 4) + 4 * g16 + e % 4;
                     const uint32_t bo = blk_off(rv * S::RB + cc * S::EB);
-                    if constexpr (T == kI8) {
-                        vbp[t][0][e] = (_Float16)(int)*(const int8_t *)(reg + bo);
-                    } else {
-                        _Float16 hi, lo;
-                        split_hl(*(const float *)(reg + bo), hi, lo);
-                        vbp[t][0][e] = hi;
-                        vbp[t][1][e] = lo;
-                    }
+                    _Float16 hi, lo;
+                    split_hl(*(const float *)(reg + bo), hi, lo);
+                    vbp[t][0][e] = hi;
+                    vbp[t][1][e] = lo;
                 }
             }
         }
