@@ -287,7 +287,7 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
             if (rc)
                 return rc;
             d.wg0 = wg;
-            uint64_t nwg = (uint64_t)a->n_kv * prefill_row_blocks(d.n, a->group);
+            uint64_t nwg = (uint64_t)a->n_kv * prefill_row_blocks(d.n, a->group, a->hd);
             if (wg + nwg > 0x7FFFFFFFu)
                 return JANAS_ATTN_ERANGE;
             wg += (uint32_t)nwg;

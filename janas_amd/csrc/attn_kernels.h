@@ -122,7 +122,7 @@ hipError_t launch_q8k(const Q8kArgs &a, hipStream_t s);
 hipError_t launch_prefill(int kv, const PrefillArgs &a, hipStream_t s);
 int prefill_supported(int kv, uint32_t hd);
 /* prefill workgroups a KV head of an n-token sequence takes */
-uint32_t prefill_row_blocks(uint32_t n, uint32_t group);
+uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd);
 
 }  // namespace janas
 

@@ -12,7 +12,8 @@
  *
  *   workgroup   8 waves, 256 query rows = 64 tokens x the 4 (or G) query
  *               heads of one KV head, so each K/V tile is read once for the
- *               whole GQA group. Row blocks of later tokens (more keys to
+ *               whole GQA group (head size 256: 4 waves, 128 rows, one wave
+ *               a SIMD with 512 registers, and 64-position key tiles). Row blocks of later tokens (more keys to
  *               see) are dispatched first; consecutive workgroups share a KV
  *               head, so they share an XCD's L2.
  *   key tiles   128 positions of K and V in LDS, two buffers; the next
@@ -65,11 +66,17 @@ typedef float f16x __attribute__((ext_vector_type(16)));
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-constexpr int kPWaves = 8;                 /* waves a workgroup */
 constexpr int kPRows = 32;                 /* query rows a wave */
-constexpr int kPBlock = kPWaves * kPRows;  /* query rows a workgroup */
-constexpr int kTile = 128;                 /* key positions a tile */
-constexpr int kNPB = kTile / 32;           /* blocks of 32 positions a tile */
+
+/* waves a workgroup and key positions a tile: 8 and 128 up to head size
+   128; 4 (one a SIMD, 512 registers: a 256-column row's output alone is
+   128 of them) and 64 (LDS) at 256 */
+template <int D> struct PCfg {
+    static constexpr int W = D > 128 ? 4 : 8;
+    static constexpr int TILE = D > 128 ? 64 : 128;
+    static constexpr int NPB = TILE / 32;   /* blocks of 32 positions a tile */
+    static constexpr int BLOCK = W * kPRows; /* query rows a workgroup */
+};
 constexpr float kLog2e = 1.4426950408889634f;
 /* a row's weights are exp2(s - m) against a maximum m that is only moved
    when a score passes it by more than this (so weights stay below 2^8,
@@ -161,8 +168,8 @@ template <int D> struct PShape {
     static constexpr int KS = D / 16;  /* score k-steps */
     static constexpr int CT = D / 32;  /* output column tiles */
     /* a tile's 16-byte units of K (and of V), and a thread's share */
-    static constexpr int UNITS = kTile * D * 2 / 16;
-    static constexpr int UPT = UNITS / (kPWaves * 64);
+    static constexpr int UNITS = PCfg<D>::TILE * D * 2 / 16;
+    static constexpr int UPT = UNITS / (PCfg<D>::W * 64);
     static constexpr int UPR = D * 2 / 16;  /* units a row */
 };
 
@@ -184,8 +191,10 @@ struct PBlock {
     uint32_t rlo, rhi;         /* the positions it sees */
 };
 
+template <int D>
 __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
 {
+    constexpr int kPBlock = PCfg<D>::BLOCK, kTile = PCfg<D>::TILE;
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t l32 = lane & 31;
     const uint32_t id = xcd_remap(blockIdx.x, gridDim.x);
@@ -257,6 +266,7 @@ __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8
                                           float &m, float &lsum, f16x *o,
                                           KOp kop, VOp vop)
 {
+    constexpr int kNPB = PCfg<D>::NPB, kTile = PCfg<D>::TILE;
     constexpr int KS = D / 16, CT = D / 32;
     const uint32_t g = (threadIdx.x & 63) >> 5;
     /* scores less the row's maximum so far (the accumulators start at
@@ -441,17 +451,18 @@ __device__ __forceinline__ size_t cache_row(const PBlock &P, uint32_t cap, bool 
  * them into padded LDS rows (K pitch D + 8, V pitch D + 16 halves).
  */
 template <int T, int D>
-__global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs A)
+__global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_kernel(const PrefillArgs A)
 {
     using S = PShape<D>;
     using E = PElem<T>;
+    constexpr int kPWaves = PCfg<D>::W, kTile = PCfg<D>::TILE;
     static_assert(S::UPT >= 1 && S::UNITS % (kPWaves * 64) == 0, "tile loads");
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][kTile][S::KP];
     __shared__ __attribute__((aligned(16))) _Float16 sV[2][kTile][S::VP];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t g = lane >> 5, l32 = lane & 31, l16 = lane & 15;
-    const PBlock P = block_of(A);
+    const PBlock P = block_of<D>(A);
     const SeqDesc &sq = *P.sq;
     const uint32_t hd = A.hd;
     const bool ring = A.ring != 0;
@@ -554,7 +565,8 @@ __device__ __forceinline__ uint32_t swz(uint32_t r)
 template <int D>
 __global__ __launch_bounds__(512) void prefill_dma_kernel(const PrefillArgs A)
 {
-    static_assert(D == 128, "rows of 16 units");
+    static_assert(D == 128 && PCfg<D>::W == 8, "rows of 16 units, 8 waves");
+    constexpr uint32_t kTile = PCfg<D>::TILE;
     constexpr uint32_t RB = D * 2;        /* bytes a row */
     constexpr uint32_t TB = kTile * RB;   /* bytes a tile */
     constexpr int CT = D / 32;
@@ -565,7 +577,7 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const PrefillArgs A)
 
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t g = lane >> 5, l32 = lane & 31, l16 = lane & 15;
-    const PBlock P = block_of(A);
+    const PBlock P = block_of<D>(A);
     const SeqDesc &sq = *P.sq;
     const uint32_t hd = A.hd;
     const bool ring = A.ring != 0;
@@ -660,7 +672,7 @@ hipError_t launch_d(const PrefillArgs &a, hipStream_t s)
     if constexpr (T == kF16 && D == 128)
         hipLaunchKernelGGL((prefill_dma_kernel<D>), dim3(a.n_wg), dim3(512), 0, s, a);
     else
-        hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(a.n_wg), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(a.n_wg), dim3(PCfg<D>::W * 64), 0, s, a);
     return hipGetLastError();
 }
 
@@ -671,6 +683,8 @@ hipError_t launch_t(const PrefillArgs &a, hipStream_t s)
         return launch_d<T, 64>(a, s);
     if (a.hd <= 128)
         return launch_d<T, 128>(a, s);
+    if (a.hd <= 256)
+        return launch_d<T, 256>(a, s);
     return hipErrorInvalidValue;
 }
 
@@ -679,13 +693,14 @@ hipError_t launch_t(const PrefillArgs &a, hipStream_t s)
 int prefill_supported(int kv, uint32_t hd)
 {
     return (kv == kF16 || kv == kI8 || kv == kI16) && hd >= 8 && hd % 8 == 0 &&
-           hd <= 128;
+           hd <= 256;
 }
 
-uint32_t prefill_row_blocks(uint32_t n, uint32_t group)
+uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd)
 {
-    /* a workgroup takes kPBlock of a KV head's n x group rows */
-    return (uint32_t)(((uint64_t)n * group + kPBlock - 1) / kPBlock);
+    /* a workgroup takes PCfg::BLOCK of a KV head's n x group rows */
+    const uint64_t block = hd > 128 ? PCfg<256>::BLOCK : PCfg<128>::BLOCK;
+    return (uint32_t)(((uint64_t)n * group + block - 1) / block);
 }
 
 hipError_t launch_prefill(int kv, const PrefillArgs &a, hipStream_t s)

@@ -117,6 +117,11 @@ SHAPES = {
     "g2_hd40_window_long": (4, 2, 40, 2048, 700, 1200, 513, 0.3),
     "g5_hd120_n65": (10, 2, 120, 300, 65, 200, 0, None),
     "g16_hd64": (16, 1, 64, 600, 257, 300, 0, None),
+    # head size 256 (4 waves, 64-position tiles): config 4's heads, a
+    # window, and 200 columns (the last tiles partly past the row)
+    "g8_hd256_cfg4": (16, 2, 256, 1100, 700, 300, 0, 1.0 / 16),
+    "g4_hd256_window": (8, 2, 256, 900, 257, 600, 300, None),
+    "g3_hd200": (6, 2, 200, 500, 130, 100, 0, None),
 }
 
 
@@ -234,7 +239,9 @@ def quantized(seed, n_kv, cap, hd, wide):
                                        n=333, pos0=500, window=300),
                                   dict(n_head=8, n_kv=1, hd=96, cap=768,
                                        n=200, pos0=600, window=200,
-                                       ring=True)])
+                                       ring=True),
+                                  dict(n_head=16, n_kv=2, hd=256, cap=800,
+                                       n=500, pos0=100)])
 def test_prefill_quantized_cache(gpu, wide, geom):
     """int8 / int16 caches with their scales (the engine's own format) on
     the MFMA path: rows dequantized into f16 as tiles are staged; the bar is
@@ -267,10 +274,10 @@ def test_prefill_quantized_cache(gpu, wide, geom):
 
 
 def test_prefill_refuses_what_it_has_no_kernel_for(gpu):
-    """f32 caches and head sizes above 128 have no prefill kernel:
+    """f32 caches and head sizes above 256 have no prefill kernel:
     janas_attn_run_dev_prefill says ENOTSUP, janas_attn_run_dev takes the
     split path."""
-    h, kvh, hd, cap, n = 4, 2, 256, 300, 100
+    h, kvh, hd, cap, n = 4, 2, 512, 300, 100
     s = dict(k=cache(301, kvh, cap, hd, np.float16),
              v=cache(302, kvh, cap, hd, np.float16),
              q=normal(303, n * h * hd).reshape(n, h, hd), pos0=0, n=n)
