@@ -1,7 +1,7 @@
 """Benchmark of the KV-cache attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                    [--only decode|prefill|wide|copy]
+                    [--only decode|prefill|wide|copy|gemm]
 
 Headline (BASELINE.json metric): decode attention KV GB/s at 32k context on
 BASELINE config 4 - 16 query / 2 KV heads, head_dim 256, 32,768 positions,
@@ -14,7 +14,11 @@ rides along in the same line under "prefill": one causal call over an
 (token, head, position)) over the launch time. Under "wide": Gemma 4's
 head size - a decode step at 32k over an int16 cache with head_dim 512
 (16 / 2 heads, the reference test's score scale 0.02), the wide kernel's
-KV bytes (and scales) over its launch time.
+KV bytes (and scales) over its launch time. Beside the prefill, under
+"reference_gemm": a plain f16 GEMM through the vendor library (torch.matmul,
+8192^3, N(0, 1) operands) on the same box - the practical MFMA rate that
+random data allows (the clock falls well below its 2.4 GHz peak under
+random operands), as a yardstick for the prefill's fraction of 2.5 PFLOP/s.
 
 Prints one JSON line. ``roofline`` is the split kernel's: its algorithmic
 bytes (every K/V element of the visible positions once) over its average
@@ -228,6 +232,32 @@ def bench_prefill(torch, jm, w, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
+def bench_gemm(torch, n=8192, steps=10, warmup=3):
+    """f16 GEMM of two random N(0, 1) n x n matrices through torch.matmul
+    (the vendor library): TFLOP/s over launches timed with HIP events on
+    torch's current stream, where they run."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(SEED + 9)
+    a = torch.randn(n, n, generator=g, device=dev, dtype=torch.float32).half()
+    b = torch.randn(n, n, generator=g, device=dev, dtype=torch.float32).half()
+    for _ in range(warmup):
+        c = torch.matmul(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(
+        enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        c = torch.matmul(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    del a, b, c
+    return {"what": f"torch.matmul f16 {n}x{n}x{n}, N(0,1) operands",
+            "value": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1),
+            "unit": "TFLOP/s", "ms": round(ms, 4)}
+
+
 def bench_copy(torch, steps):
     """A plain 64 MiB device copy: the known-size kernel that scales the
     HBM byte counters (FETCH_SIZE, WRITE_SIZE) of a profile."""
@@ -274,7 +304,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=("decode", "prefill", "wide", "copy"),
+    ap.add_argument("--only", choices=("decode", "prefill", "wide", "copy",
+                                       "gemm"),
                     help="run one leg alone (profiling)")
     ap.add_argument("--prefill-steps", type=int, default=20)
     args = ap.parse_args()
@@ -290,6 +321,9 @@ def main():
 
     if args.only == "copy":
         bench_copy(torch, args.steps)
+        return
+    if args.only == "gemm":
+        print(json.dumps(bench_gemm(torch)), flush=True)
         return
     if args.only == "prefill":
         wp = prefill_workload()
@@ -353,6 +387,9 @@ def main():
                      "traffic": traffic_from_profiles("prefill_dma_kernel_8k"),
                      "kernel": "prefill_dma_kernel<128>"},
     }
+    gemm = bench_gemm(torch)
+    gemm["prefill_over_gemm"] = round(tf / gemm["value"], 4)
+    line["prefill"]["reference_gemm"] = gemm
     line["wide"] = wide_leg(torch, jm, max(1, args.steps // 4),
                             min(args.warmup, 20))
     if not args.no_cpu:

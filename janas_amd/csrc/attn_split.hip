@@ -539,6 +539,20 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
        are inside the row or none is) */
     const uint32_t col = db * kCols + CPL * cl;
     const bool colok = col < hd;
+    /* the gate, asked for before the partials so the two loads overlap */
+    const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
+    float4 gv = {0.0f, 0.0f, 0.0f, 0.0f};
+    float gh = 0.0f;
+    if (g == 0 && colok) {
+        if (A.gate_mode == kGateElem) {
+            if constexpr (CPL == 4)
+                gv = *(const float4 *)(sq.gate + oi);
+            else
+                gv.x = sq.gate[oi];
+        } else if (A.gate_mode == kGateHead) {
+            gh = sq.gate[(size_t)j * A.n_head + h];
+        }
+    }
     float mg = -INFINITY, lg = 0.0f;
     float4 ag = {0.0f, 0.0f, 0.0f, 0.0f};
     for (uint32_t i0 = g; i0 < nc; i0 += kMergeGroups * kMergeBatch) {
@@ -602,16 +616,6 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     }
     const float sum = ((wl[0] + wl[1]) + (wl[2] + wl[3])) + ((wl[4] + wl[5]) + (wl[6] + wl[7]));
     const float inv = 1.0f / sum;
-    const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
-    float4 gv = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (A.gate_mode == kGateElem) {
-        if constexpr (CPL == 4)
-            gv = *(const float4 *)(sq.gate + oi);
-        else
-            gv.x = sq.gate[oi];
-    }
-    const float gh = A.gate_mode == kGateHead
-                         ? sq.gate[(size_t)j * A.n_head + h] : 0.0f;
     float4 o;
 #pragma unroll
     for (int e = 0; e < CPL; e++) {
