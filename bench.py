@@ -1,7 +1,7 @@
 """Benchmark of the KV-cache attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                    [--only decode|prefill|wide|copy|gemm]
+                    [--only decode|prefill|wide|copy|gemm|configs]
 
 Headline (BASELINE.json metric): decode attention KV GB/s at 32k context on
 BASELINE config 4 - 16 query / 2 KV heads, head_dim 256, 32,768 positions,
@@ -19,6 +19,11 @@ KV bytes (and scales) over its launch time. Beside the prefill, under
 8192^3, N(0, 1) operands) on the same box - the practical MFMA rate that
 random data allows (the clock falls well below its 2.4 GHz peak under
 random operands), as a yardstick for the prefill's fraction of 2.5 PFLOP/s.
+Under "configs": the other BASELINE configurations, each timed as the
+calls the engine makes, through the library's own routing
+(janas_attn_run_dev): 1 (f32 decode at 1k, launch-bound), 2 (causal prefill
+of 1,024 tokens), 3 (ragged decode of 8 sequences), 5a (verify of 8 drafts
+at 8k) and 5b (an 8k prompt as 16 chunks of 512).
 
 Prints one JSON line. ``roofline`` is the split kernel's: its algorithmic
 bytes (every K/V element of the visible positions once) over its average
@@ -258,6 +263,103 @@ def bench_gemm(torch, n=8192, steps=10, warmup=3):
             "unit": "TFLOP/s", "ms": round(ms, 4)}
 
 
+def _timed(torch, fns, steps, warmup, stream):
+    """ms per call of fns (rotating), HIP events on the calls' stream."""
+    for i in range(warmup):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(
+        enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        fns[i % len(fns)]()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def configs_leg(torch, jm, steps=200, warmup=20):
+    """BASELINE configs 1, 2, 3, 5a and 5b (synthetic N(0, 1), seeded):
+    one call (5b: the 16 chunk calls) through janas_attn_run_dev, on a
+    stream of its own. Decode-like configs rotate over enough cache copies
+    to exceed the 256 MB infinity cache (config 1's 8 MB is launch-bound
+    by design and is not rotated)."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    h, kvh, hd = 32, 8, 128
+    res = {}
+
+    def dev_t(x):
+        return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+    def decode_like(name, rng, kv, dtype, lens, n, ncopy, workload):
+        cap = max(lens)
+        seqs_np = [dict(k=normal(rng, (kvh, L, hd), dtype),
+                        v=normal(rng, (kvh, L, hd), dtype),
+                        q=normal(rng, (n, h, hd), np.float32), L=L)
+                   for L in lens]
+        copies = []
+        for _ in range(ncopy):
+            copies.append([dict(k=dev_t(x["k"]), v=dev_t(x["v"]),
+                                q=dev_t(x["q"]),
+                                out=torch.empty((n, h, hd), device=dev),
+                                cap=x["L"], n=n, pos0=x["L"] - n)
+                           for x in seqs_np])
+        a = jm.Attention(h, kvh, hd, cap)
+        fns = [a.prepare(kv, c, stream=stream.cuda_stream) for c in copies]
+        ms = _timed(torch, fns, steps, warmup, stream)
+        a.close()
+        esz = np.dtype(dtype).itemsize
+        kv_bytes = sum(2 * kvh * L * hd * esz for L in lens)
+        gbs = kv_bytes / (ms * 1e-3) / 1e9
+        res[name] = {"workload": workload, "ms": round(ms, 5),
+                     "value": round(gbs, 1), "unit": "GB/s",
+                     "kv_bytes": kv_bytes, "bound": "hbm",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+    rng = np.random.default_rng(SEED + 21)
+    decode_like("1", rng, jm.KV_F32, np.float32, [1024], 1, 1,
+                "decode, 32 Q / 8 KV heads, head_dim 128, 1024 positions, "
+                "f32 K/V and q (launch-bound)")
+    rng = np.random.default_rng(SEED + 23)
+    lens = [int(x) for x in rng.integers(512, 8193, 8)]
+    decode_like("3", rng, jm.KV_F16, np.float16, lens, 1, 2,
+                f"ragged decode, 8 sequences of {lens} positions, 32 / 8 "
+                "heads, head_dim 128, f16 K/V, f32 q, one call")
+    rng = np.random.default_rng(SEED + 25)
+    decode_like("5a", rng, jm.KV_F16, np.float16, [8200], 8, 8,
+                "verify: 8 drafts at positions 8192..8199 over the cache, "
+                "32 / 8 heads, head_dim 128, f16 K/V, f32 q")
+
+    def prefill_like(name, rng, L, chunk, reps, workload):
+        k = dev_t(normal(rng, (kvh, L, hd), np.float16))
+        v = dev_t(normal(rng, (kvh, L, hd), np.float16))
+        q = dev_t(normal(rng, (L, h, hd), np.float32))
+        out = torch.empty_like(q)
+        a = jm.Attention(h, kvh, hd, L)
+        fns = [a.prepare(jm.KV_F16, [dict(
+            k=k, v=v, q=q[c:c + chunk], out=out[c:c + chunk], cap=L,
+            n=chunk, pos0=c)], stream=stream.cuda_stream)
+            for c in range(0, L, chunk)]
+        ncall = len(fns)
+        ms = _timed(torch, fns, reps * ncall, 2 * ncall, stream) * ncall
+        a.close()
+        fl = prefill_flops(hd, h, 0, L)
+        tf = fl / (ms * 1e-3) / 1e12
+        res[name] = {"workload": workload, "ms": round(ms, 5),
+                     "value": round(tf, 2), "unit": "TFLOP/s", "flops": fl,
+                     "bound": "mfma", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+
+    prefill_like("2", np.random.default_rng(SEED + 22), 1024, 1024, 50,
+                 "causal prefill, 1024 tokens, 32 / 8 heads, head_dim 128, "
+                 "f16 K/V, f32 q")
+    prefill_like("5b", np.random.default_rng(SEED + 26), 8192, 512, 10,
+                 "chunked prefill: an 8192-token prompt as 16 calls of 512 "
+                 "(pos0 = 512 c) over the growing cache, 32 / 8 heads, "
+                 "head_dim 128, f16 K/V, f32 q")
+    return res
+
+
 def bench_copy(torch, steps):
     """A plain 64 MiB device copy: the known-size kernel that scales the
     HBM byte counters (FETCH_SIZE, WRITE_SIZE) of a profile."""
@@ -305,7 +407,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=("decode", "prefill", "wide", "copy",
-                                       "gemm"),
+                                       "gemm", "configs"),
                     help="run one leg alone (profiling)")
     ap.add_argument("--prefill-steps", type=int, default=20)
     args = ap.parse_args()
@@ -324,6 +426,9 @@ def main():
         return
     if args.only == "gemm":
         print(json.dumps(bench_gemm(torch)), flush=True)
+        return
+    if args.only == "configs":
+        print(json.dumps(configs_leg(torch, jm)), flush=True)
         return
     if args.only == "prefill":
         wp = prefill_workload()
@@ -392,6 +497,7 @@ def main():
     line["prefill"]["reference_gemm"] = gemm
     line["wide"] = wide_leg(torch, jm, max(1, args.steps // 4),
                             min(args.warmup, 20))
+    line["configs"] = configs_leg(torch, jm)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_decode_baseline(w)
         line["prefill"]["cpu_baseline"] = cpu_prefill_baseline(wp)

@@ -156,9 +156,13 @@ struct janas_attn_q8k {
  * instance's own), asynchronous. The instance's geometry, scale, window and
  * ring apply to all. Blocks of up to JANAS_ATTN_MAX_BLOCK tokens a sequence
  * take the split-KV path, whose chunking matches janas_attn_run bit for bit
- * token by token; longer prompts take the MFMA prefill path (causal tiles,
- * no partials), equal within the f16 tolerance. The instance's partials are
- * grown as needed; one call at a time per instance.
+ * token by token; longer prompts take the MFMA prefill path (causal tiles),
+ * equal within the f16 tolerance. A prompt whose row blocks alone would
+ * leave compute units idle (a short prompt, a chunk of a long one) has its
+ * key range split into segments, merged in order through the partials; the
+ * split depends on the sequence alone, so its result is the same in any
+ * launch. The instance's partials are grown as needed; one call at a time
+ * per instance.
  */
 int janas_attn_run_dev(struct janas_attn *a, int kv_type, int gate_mode,
                        const struct janas_attn_seq *seqs, uint32_t n_seqs,

@@ -38,6 +38,7 @@ struct janas_attn {
     int kv16, ring;
     const uint32_t *last; /* host, the next janas_attn_run only */
     int dev;
+    uint32_t cus;         /* compute units of the device */
     hipStream_t stream;
     /* partials: part_rows rows of (m, l) and of hd values */
     float *part_ml, *part_acc;
@@ -271,6 +272,28 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
     return JANAS_ATTN_OK;
 }
 
+/* Key segments for a prefill sequence whose row blocks alone would leave
+   compute units idle (a short prompt, a chunk of a long one): enough to
+   give each unit a workgroup, at least kSegTiles key tiles each. It
+   depends on the sequence alone, so a sequence's result is the same in
+   any launch. */
+constexpr uint32_t kSegTiles = 6, kMaxSeg = 16;
+
+uint32_t prefill_segments(const janas_attn *a, const SeqDesc &d)
+{
+    const uint64_t blocks = (uint64_t)a->n_kv * prefill_row_blocks(d.n, a->group, a->hd);
+    if (blocks >= a->cus)
+        return 1;
+    /* the key tiles of the latest row block, which sees the most */
+    const uint32_t tile = prefill_tile(a->hd);
+    const uint32_t last = d.pos0 + d.n - 1;
+    const uint32_t lo = a->window && last + 1 > a->window ? last + 1 - a->window : 0;
+    const uint32_t nt = (d.end - 1) / tile - lo / tile + 1;
+    uint64_t want = (a->cus + blocks - 1) / blocks;
+    want = std::min<uint64_t>(want, std::max<uint32_t>(1, nt / kSegTiles));
+    return (uint32_t)std::min<uint64_t>(want, kMaxSeg);
+}
+
 int run_prefill(janas_attn *a, int kv, int gate_mode,
                 const janas_attn_seq *seqs, uint32_t n_seqs, hipStream_t stream)
 {
@@ -280,18 +303,38 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
         uint32_t m = std::min(kMaxSeqs, n_seqs - s0);
         PrefillArgs args;
         memset(&args, 0, sizeof args);
-        uint32_t wg = 0;
+        uint32_t wg = 0, mg = 0;
+        uint64_t rows = 0;
         for (uint32_t i = 0; i < m; i++) {
             SeqDesc &d = args.seq[i];
             int rc = describe(a, kv, seqs[s0 + i], d);
             if (rc)
                 return rc;
             d.wg0 = wg;
-            uint64_t nwg = (uint64_t)a->n_kv * prefill_row_blocks(d.n, a->group, a->hd);
-            if (wg + nwg > 0x7FFFFFFFu)
+            d.mg0 = mg;
+            d.nseg = prefill_segments(a, d);
+            d.part0 = 0;
+            uint64_t nwg = (uint64_t)a->n_kv * d.nseg *
+                           prefill_row_blocks(d.n, a->group, a->hd);
+            uint64_t nmg = 0;
+            if (d.nseg > 1) {
+                /* partial rows from part0: (token, head) major, segment minor */
+                d.part0 = rows;
+                rows += (uint64_t)d.n * a->n_head * d.nseg;
+                nmg = ((uint64_t)d.n * a->n_head + kPMergeRows - 1) / kPMergeRows;
+            }
+            if (wg + nwg > 0x7FFFFFFFu || mg + nmg > 0x7FFFFFFFu)
                 return JANAS_ATTN_ERANGE;
             wg += (uint32_t)nwg;
+            mg += (uint32_t)nmg;
         }
+        if (rows) {
+            int rc = ensure_part(a, rows, stream);
+            if (rc)
+                return rc;
+        }
+        args.part_ml = a->part_ml;
+        args.part_acc = a->part_acc;
         args.n_seqs = m;
         args.n_wg = wg;
         args.n_head = a->n_head;
@@ -304,6 +347,8 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
         args.gate_mode = gate_mode;
         ProfEv *ev = prof_begin(a, 2, stream);
         hipError_t e = launch_prefill(kv, args, stream);
+        if (e == hipSuccess && mg)
+            e = launch_prefill_merge(args, mg, stream);
         prof_end(ev, stream);
         if (e != hipSuccess)
             return hip_err(e, "prefill launch");
@@ -370,6 +415,13 @@ extern "C" struct janas_attn *janas_attn_create(uint32_t n_head,
     a->n_ctx = n_ctx;
     a->group = n_head / n_head_kv;
     a->dev = dev;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+            hipSuccess || cus < 1) {
+        (void)hipGetLastError();
+        cus = 256;
+    }
+    a->cus = (uint32_t)cus;
     a->scale = 1.0f / sqrtf((float)head_dim);
     /* attention.c:965-982: JANAS_ATTN overrides the asked way */
     const char *e = getenv("JANAS_ATTN");

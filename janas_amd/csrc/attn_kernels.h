@@ -39,7 +39,8 @@ struct SeqDesc {
     uint32_t rtiles;       /* query-row tiles of 16 (rows = n x group) */
     uint32_t wg0;          /* first workgroup of the split launch */
     uint32_t mg0;          /* first workgroup of the merge launch */
-    uint32_t pad_;
+    uint32_t nseg;         /* prefill: key segments a row block is split
+                              into (1: none, the output is written directly) */
     uint64_t part0;        /* first partial row (of m, l and hd values) */
 };
 
@@ -59,6 +60,9 @@ struct SplitArgs {
 /* The causal MFMA pass over whole prompts (prefill, chunked prefill). */
 struct PrefillArgs {
     SeqDesc seq[kMaxSeqs];
+    float *part_ml;        /* split sequences: [partial rows][2] */
+    float *part_acc;       /* [partial rows][hd]; a sequence's start at its
+                              part0, (token, head) major, segment minor */
     uint32_t n_seqs, n_wg;
     uint32_t n_head, n_kv, group, hd, window;
     float scale;
@@ -121,8 +125,14 @@ hipError_t launch_q8k(const Q8kArgs &a, hipStream_t s);
 /* attn_prefill.hip */
 hipError_t launch_prefill(int kv, const PrefillArgs &a, hipStream_t s);
 int prefill_supported(int kv, uint32_t hd);
-/* prefill workgroups a KV head of an n-token sequence takes */
+/* row blocks a KV head of an n-token sequence takes (one workgroup each
+   per key segment), and the key positions a tile */
 uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd);
+uint32_t prefill_tile(uint32_t hd);
+/* the ordered merge of split sequences' segment partials: n_wg workgroups
+   of kPMergeRows rows (a row is one (token, head)) */
+constexpr uint32_t kPMergeRows = 4;
+hipError_t launch_prefill_merge(const PrefillArgs &a, uint32_t n_wg, hipStream_t s);
 
 }  // namespace janas
 

@@ -42,6 +42,13 @@
  *               stays in the lane that holds its softmax state.
  *   masks       only the tiles a row's range cuts; tiles wholly outside
  *               every row's range are not visited.
+ *   segments    a call whose row blocks alone would leave compute units
+ *               idle (a short prompt, a 512-token chunk of a long one)
+ *               splits each block's key tiles into nseg contiguous
+ *               segments, one workgroup each; a segment leaves its rows'
+ *               partials (m, sum, unnormalised values) and pmerge_kernel
+ *               folds them in segment order. nseg is the host's choice per
+ *               sequence (attn_api.cpp), from the sequence alone.
  *   epilogue    O / sum, the output gate sigmoid(g) * o (model_attn.c:
  *               159-170) fused in.
  *
@@ -184,7 +191,8 @@ template <int D> struct PShape {
 struct PBlock {
     const SeqDesc *sq;
     uint32_t lo_all, hi_all;   /* positions any row of the block sees */
-    uint32_t tfirst, tlast;    /* key tiles visited */
+    uint32_t tfirst, tlast;    /* key tiles visited (the segment's) */
+    uint32_t seg, nseg;        /* the key segment, of nseg (1: not split) */
     size_t head_row;           /* the KV head's first cache row */
     bool rok;                  /* the lane's row exists */
     uint32_t rj, rh;           /* its token and query head */
@@ -207,9 +215,13 @@ __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
     const uint32_t G = A.group;
     const uint32_t R = sq.n * G;
     const uint32_t nrb = (R + kPBlock - 1) / kPBlock;
+    /* a KV head's workgroups: row blocks, the longest rows first, each
+       split into nseg key segments */
+    const uint32_t nseg = sq.nseg;
     const uint32_t local = id - sq.wg0;
-    const uint32_t kvh = local / nrb;
-    const uint32_t rb = nrb - 1 - local % nrb; /* the longest rows first */
+    const uint32_t kvh = local / (nrb * nseg);
+    const uint32_t rem = local % (nrb * nseg);
+    const uint32_t rb = nrb - 1 - rem / nseg;
     const uint32_t r0 = rb * kPBlock;
 
     /* the block's rows see [lo(first token), hi(last token)] */
@@ -220,14 +232,29 @@ __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
     P.hi_all = sq.last ? sq.end - 1 : sq.pos0 + jl;
     P.tfirst = P.lo_all / kTile;
     P.tlast = P.hi_all / kTile;
+    /* segment seg: tiles tfirst + [seg nt / nseg, (seg + 1) nt / nseg). An
+       empty one (a block with fewer tiles than segments) runs its first
+       tile with every row masked, which leaves the neutral partial
+       (m = -inf, no weight) - no branch around the tile loop */
+    P.seg = rem % nseg;
+    P.nseg = nseg;
+    bool empty = false;
+    if (nseg > 1) {
+        const uint64_t nt = P.tlast - P.tfirst + 1;
+        const uint32_t a = P.tfirst + (uint32_t)(P.seg * nt / nseg);
+        const uint32_t b = P.tfirst + (uint32_t)((P.seg + 1) * nt / nseg);
+        empty = a == b;
+        P.tfirst = a;
+        P.tlast = empty ? a : b - 1;
+    }
     P.head_row = (size_t)kvh * sq.cap;
 
     const uint32_t r = r0 + kPRows * w + l32;
     P.rok = r < R;
     P.rj = (P.rok ? r : r0) / G;
     P.rh = kvh * G + (P.rok ? r : r0) % G;
-    P.rlo = P.rok ? row_lo(A, sq.pos0 + P.rj) : 1;
-    P.rhi = P.rok ? (sq.last ? sq.last[P.rj] : sq.pos0 + P.rj) : 0;
+    P.rlo = P.rok && !empty ? row_lo(A, sq.pos0 + P.rj) : 1;
+    P.rhi = P.rok && !empty ? (sq.last ? sq.last[P.rj] : sq.pos0 + P.rj) : 0;
     return P;
 }
 
@@ -432,6 +459,37 @@ __device__ __forceinline__ void write_out(const PrefillArgs &A, const PBlock &P,
         }
 }
 
+/* the lane's row when its row block is split into key segments: the
+   segment's partial - largest score m (log2 units, -inf when the row saw
+   nothing of it), sum of weights, unnormalised weighted values - for the
+   ordered merge (pmerge_kernel); otherwise the output itself */
+template <int D>
+__device__ __forceinline__ void finish(const PrefillArgs &A, const PBlock &P,
+                                       float m, float lsum, const f16x *o)
+{
+    if (P.nseg == 1) {
+        write_out<D>(A, P, lsum, o);
+        return;
+    }
+    const uint32_t g = (threadIdx.x & 63) >> 5, hd = A.hd;
+    const float lt = lsum + __shfl_xor(lsum, 32, 64);
+    if (!P.rok)
+        return;
+    const size_t pr = P.sq->part0 + ((size_t)P.rj * A.n_head + P.rh) * P.nseg + P.seg;
+    if (g == 0)
+        *(float2 *)(A.part_ml + 2 * pr) = float2{m, lt};
+    float *dst = A.part_acc + pr * hd;
+#pragma unroll
+    for (int c = 0; c < D / 32; c++)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const uint32_t col = 32 * c + 8 * q4 + 4 * g;
+            if (col < hd)
+                *(float4 *)(dst + col) = float4{o[c][4 * q4], o[c][4 * q4 + 1],
+                                                o[c][4 * q4 + 2], o[c][4 * q4 + 3]};
+        }
+}
+
 /* the tile position a row of the tile reads: outside [lo_all, hi_all] the
    nearest of the two (masked, but never a row the caller has not written),
    a ring's row modulo its size */
@@ -536,7 +594,7 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_kernel(const PrefillA
             __syncthreads();
         }
     }
-    write_out<D>(A, P, lsum, o);
+    finish<D>(A, P, m, lsum, o);
 }
 
 /*
@@ -663,7 +721,58 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const PrefillArgs A)
         if (tile + 2 > P.tlast)
             break;
     }
-    write_out<D>(A, P, lsum, o);
+    finish<D>(A, P, m, lsum, o);
+}
+
+/*
+ * The ordered merge of split rows: wave w of workgroup b takes row
+ * kPMergeRows b + w of its sequence (a row is one (token, head)), lane t
+ * columns 4 t .. 4 t + 3. Segments fold in order against the largest m:
+ * out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s, then the gate as in
+ * write_out.
+ */
+__global__ __launch_bounds__(kPMergeRows * 64) void pmerge_kernel(const PrefillArgs A)
+{
+    const uint32_t id = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    uint32_t si = 0;
+    while (si + 1 < A.n_seqs && A.seq[si + 1].mg0 <= id)
+        si++;
+    const SeqDesc &sq = A.seq[si];
+    const uint32_t hd = A.hd, nseg = sq.nseg;
+    const uint32_t row = (id - sq.mg0) * kPMergeRows + w;
+    if (row >= sq.n * A.n_head)
+        return;
+    const uint32_t j = row / A.n_head, h = row % A.n_head;
+    const size_t pr0 = sq.part0 + (size_t)row * nseg;
+    float mx = -INFINITY;
+    for (uint32_t s = 0; s < nseg; s++)
+        mx = fmaxf(mx, A.part_ml[2 * (pr0 + s)]);
+    const uint32_t col = 4 * lane;
+    if (col >= hd)
+        return;
+    float l = 0.0f;
+    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t s = 0; s < nseg; s++) {
+        const float2 ml = *(const float2 *)(A.part_ml + 2 * (pr0 + s));
+        const float wt = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - mx);
+        const float4 v = *(const float4 *)(A.part_acc + (pr0 + s) * hd + col);
+        l += wt * ml.y;
+        acc.x += wt * v.x;
+        acc.y += wt * v.y;
+        acc.z += wt * v.z;
+        acc.w += wt * v.w;
+    }
+    const float inv = 1.0f / l;
+    const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
+    float x[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        if (A.gate_mode == kGateElem)
+            x[e] *= 1.0f / (1.0f + expf(-sq.gate[oi + e]));
+        else if (A.gate_mode == kGateHead)
+            x[e] *= 1.0f / (1.0f + expf(-sq.gate[(size_t)j * A.n_head + h]));
+    }
+    *(float4 *)(sq.out + oi) = float4{x[0], x[1], x[2], x[3]};
 }
 
 template <int T, int D>
@@ -694,6 +803,17 @@ int prefill_supported(int kv, uint32_t hd)
 {
     return (kv == kF16 || kv == kI8 || kv == kI16) && hd >= 8 && hd % 8 == 0 &&
            hd <= 256;
+}
+
+uint32_t prefill_tile(uint32_t hd)
+{
+    return hd > 128 ? PCfg<256>::TILE : PCfg<128>::TILE;
+}
+
+hipError_t launch_prefill_merge(const PrefillArgs &a, uint32_t n_wg, hipStream_t s)
+{
+    hipLaunchKernelGGL(pmerge_kernel, dim3(n_wg), dim3(kPMergeRows * 64), 0, s, a);
+    return hipGetLastError();
 }
 
 uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd)
