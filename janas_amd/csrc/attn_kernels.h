@@ -20,7 +20,7 @@ constexpr uint32_t kChunk = 256;
 constexpr uint32_t kMaxSeqs = 16;
 /* merge workgroups a launch keeps at least when it takes 128 columns a
    workgroup (merge_cols) */
-constexpr uint64_t kMergeFill = 512;
+constexpr uint64_t kMergeFill = 256;
 
 enum KvType : int { kI8 = 0, kI16 = 1, kF16 = 2, kF32 = 3 };
 enum GateMode : int { kGateNone = 0, kGateElem = 1, kGateHead = 2 };
