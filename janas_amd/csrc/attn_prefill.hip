@@ -21,7 +21,7 @@
  *               64 positions: the tile's fixed costs (barriers, the row
  *               maximum's exchange) spread over twice the products (+3 %).
  *               Two kernels differ only in how a tile reaches LDS:
- *               prefill_dma_kernel (f16, head sizes 72..128) loads it
+ *               prefill_dma_kernel (f16, head sizes 72..256) loads it
  *               straight from memory into XOR-swizzled LDS rows
  *               (global_load_lds_dwordx4; one barrier a tile) and keeps its
  *               operand reads a k-step ahead of the products;
@@ -598,17 +598,21 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_kernel(const PrefillA
 }
 
 /*
- * The f16 kernel for head sizes 72..128: the next tile goes straight from
+ * The f16 kernel for head sizes 72..256: the next tile goes straight from
  * HBM (or L2) into LDS with global_load_lds_dwordx4 while this tile is
  * computed - no staging registers, no LDS stores, one barrier a tile.
  *
- * A tile is 128 rows of 256 bytes, unpadded; the 16-byte unit u of row r is
- * kept in slot u ^ swz(r), swz(r) = rotl4(r mod 16). A load instruction
- * fills 1 KB (4 rows) contiguously, so lane i fetches the unit that belongs
- * in its slot. The swizzle keeps both operand reads free of bank conflicts:
- * a score operand reads one unit of 16 consecutive rows (swz is a bijection
- * on them), a transposed value read two neighbouring units of 4 consecutive
- * rows (swz(r) >> 1 differs across the 4, so the 8 slots differ).
+ * A tile is 128 rows of 256 bytes (head size 128; 8 waves) or 64 rows of
+ * 512 (256; 4 waves, one a SIMD), unpadded; the 16-byte unit u of row r is
+ * kept in slot u ^ swz(r), swz(r) = rotl4(r mod 16), which changes the
+ * unit's low 4 bits only. A load instruction fills 1 KB (4 or 2 rows)
+ * contiguously, so lane i fetches the unit that belongs in its slot. A row
+ * is a whole number of 256-byte bank rounds, so a slot's banks depend on
+ * slot mod 16 alone, and the swizzle keeps both operand reads free of bank
+ * conflicts: a score operand reads one unit of 16 consecutive rows (swz is
+ * a bijection on them), a transposed value read two neighbouring units of 4
+ * consecutive rows (swz(r) >> 1 differs across the 4, so the 8 slots
+ * differ).
  *
  * Two buffer pairs, as distinct arrays, and the tile loop unrolled by two:
  * the compiler then sees that reads of one pair never touch the loads in
@@ -621,13 +625,17 @@ __device__ __forceinline__ uint32_t swz(uint32_t r)
 }
 
 template <int D>
-__global__ __launch_bounds__(512) void prefill_dma_kernel(const PrefillArgs A)
+__global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const PrefillArgs A)
 {
-    static_assert(D == 128 && PCfg<D>::W == 8, "rows of 16 units, 8 waves");
-    constexpr uint32_t kTile = PCfg<D>::TILE;
-    constexpr uint32_t RB = D * 2;        /* bytes a row */
-    constexpr uint32_t TB = kTile * RB;   /* bytes a tile */
+    static_assert(D == 128 || D == 256, "rows of 16 or 32 units");
+    constexpr uint32_t kW = PCfg<D>::W, kTile = PCfg<D>::TILE;
+    constexpr uint32_t RB = D * 2;              /* bytes a row */
+    constexpr uint32_t UPR = RB / 16;           /* 16-byte units a row */
+    constexpr uint32_t RPI = 64 / UPR;          /* rows a load instruction */
+    constexpr uint32_t NJ = kTile / (RPI * kW); /* load instructions a wave */
+    constexpr uint32_t TB = kTile * RB;         /* bytes a tile */
     constexpr int CT = D / 32;
+    static_assert(NJ * RPI * kW == kTile, "a tile is whole load rounds");
     __shared__ __attribute__((aligned(1024))) char sK0[TB];
     __shared__ __attribute__((aligned(1024))) char sV0[TB];
     __shared__ __attribute__((aligned(1024))) char sK1[TB];
@@ -642,12 +650,17 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const PrefillArgs A)
     h8 qb[D / 16];
     load_query<D>(A, P, qb);
 
-    /* loads: instruction j of wave w fills rows 4 (w + 8 j) .. + 3, lane i
-       row 4 (w + 8 j) + i / 16, slot i % 16; columns past hd read column 0
+    /* loads: instruction j of wave w fills the RPI rows from
+       RPI (w + W j) (1 KB), lane i row RPI (w + W j) + i / UPR, slot
+       i % UPR (the unit slot ^ swz(row)); columns past hd read column 0
        (their products meet zero query columns, or are not stored) */
-    const uint32_t drow = 4 * w + (lane >> 4);
-    const uint32_t dunit = (lane & 15) ^ swz(drow);
-    const uint32_t dcol = dunit * 8 < hd ? dunit * 8 : 0;
+    const uint32_t drow = RPI * w + lane / UPR;
+    uint32_t dcol[NJ];
+#pragma unroll
+    for (int j = 0; j < (int)NJ; j++) {
+        const uint32_t unit = (lane % UPR) ^ swz(drow + RPI * kW * j);
+        dcol[j] = unit * 8 < hd ? unit * 8 : 0;
+    }
     /* held in registers: read through P.sq inside the loop they would be
        reloaded after every load into LDS, and a pending scalar load makes
        each LDS operand wait drain the whole queue */
@@ -655,10 +668,10 @@ __global__ __launch_bounds__(512) void prefill_dma_kernel(const PrefillArgs A)
     const uint32_t cap = sq.cap;
     auto fetch = [&](uint32_t tile, char *dk, char *dv) {
 #pragma unroll
-        for (int j = 0; j < (int)(kTile / 32); j++) {
-            const size_t cr = cache_row(P, cap, ring, tile * kTile + drow + 32 * j);
-            const size_t off = cr * hd + dcol;
-            const uint32_t at = (w + 8 * j) * 1024;
+        for (int j = 0; j < (int)NJ; j++) {
+            const size_t cr = cache_row(P, cap, ring, tile * kTile + drow + RPI * kW * j);
+            const size_t off = cr * hd + dcol[j];
+            const uint32_t at = (w + kW * j) * 1024;
             __builtin_amdgcn_global_load_lds(
                 (const void *)(kg + off),
                 (__attribute__((address_space(3))) void *)(dk + at), 16, 0, 0);
@@ -778,8 +791,8 @@ __global__ __launch_bounds__(kPMergeRows * 64) void pmerge_kernel(const PrefillA
 template <int T, int D>
 hipError_t launch_d(const PrefillArgs &a, hipStream_t s)
 {
-    if constexpr (T == kF16 && D == 128)
-        hipLaunchKernelGGL((prefill_dma_kernel<D>), dim3(a.n_wg), dim3(512), 0, s, a);
+    if constexpr (T == kF16 && D >= 128)
+        hipLaunchKernelGGL((prefill_dma_kernel<D>), dim3(a.n_wg), dim3(PCfg<D>::W * 64), 0, s, a);
     else
         hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(a.n_wg), dim3(PCfg<D>::W * 64), 0, s, a);
     return hipGetLastError();
