@@ -160,7 +160,8 @@ struct janas_attn_q8k {
  * equal within the f16 tolerance. A prompt whose row blocks alone would
  * leave compute units idle (a short prompt, a chunk of a long one) has its
  * key range split into segments, merged in order through the partials; the
- * split depends on the sequence alone, so its result is the same in any
+ * split depends on the sequence and the device alone, so its result is the
+ * same in any
  * launch. The instance's partials are grown as needed; one call at a time
  * per instance.
  */

@@ -48,7 +48,8 @@
  *               segments, one workgroup each; a segment leaves its rows'
  *               partials (m, sum, unnormalised values) and pmerge_kernel
  *               folds them in segment order. nseg is the host's choice per
- *               sequence (attn_api.cpp), from the sequence alone.
+ *               sequence (attn_api.cpp), from the sequence and the
+ *               device's compute units alone.
  *   epilogue    O / sum, the output gate sigmoid(g) * o (model_attn.c:
  *               159-170) fused in.
  *
