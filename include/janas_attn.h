@@ -161,9 +161,8 @@ struct janas_attn_q8k {
  * leave compute units idle (a short prompt, a chunk of a long one) has its
  * key range split into segments, merged in order through the partials; the
  * split depends on the sequence and the device alone, so its result is the
- * same in any
- * launch. The instance's partials are grown as needed; one call at a time
- * per instance.
+ * same in any launch. The instance's partials are grown as needed; one call
+ * at a time per instance.
  */
 int janas_attn_run_dev(struct janas_attn *a, int kv_type, int gate_mode,
                        const struct janas_attn_seq *seqs, uint32_t n_seqs,
