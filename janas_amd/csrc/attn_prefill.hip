@@ -78,12 +78,18 @@ constexpr int kPRows = 32;                 /* query rows a wave */
 
 /* waves a workgroup and key positions a tile: 8 and 128 up to head size
    128; 4 (one a SIMD, 512 registers: a 256-column row's output alone is
-   128 of them) and 64 (LDS) at 256 */
+   128 of them) and 64 (LDS) at 256; at 512 the 4 waves are 2 row groups of
+   2 column halves (CS): both waves of a row group take its scores and
+   softmax, each the value product and the output of 256 columns, over
+   32-position tiles; each takes the score product over its own 256 columns
+   of the head and the two partial scores meet in LDS */
 template <int D> struct PCfg {
     static constexpr int W = D > 128 ? 4 : 8;
-    static constexpr int TILE = D > 128 ? 64 : 128;
+    static constexpr int TILE = D > 256 ? 32 : D > 128 ? 64 : 128;
     static constexpr int NPB = TILE / 32;   /* blocks of 32 positions a tile */
-    static constexpr int BLOCK = W * kPRows; /* query rows a workgroup */
+    static constexpr int CS = D > 256 ? 2 : 1;  /* column splits of a row */
+    static constexpr int OC = D / CS;       /* output columns a wave */
+    static constexpr int BLOCK = W / CS * kPRows; /* query rows a workgroup */
 };
 constexpr float kLog2e = 1.4426950408889634f;
 /* a row's weights are exp2(s - m) against a maximum m that is only moved
@@ -173,8 +179,8 @@ template <> struct PElem<kI16> {
 template <int D> struct PShape {
     static constexpr int KP = D + 8;   /* halves a K row in LDS (pitch) */
     static constexpr int VP = D + 16;  /* halves a V row in LDS */
-    static constexpr int KS = D / 16;  /* score k-steps */
-    static constexpr int CT = D / 32;  /* output column tiles */
+    static constexpr int KS = D / 16 / PCfg<D>::CS;  /* a wave's score k-steps */
+    static constexpr int CT = PCfg<D>::OC / 32;  /* a wave's output column tiles */
     /* a tile's 16-byte units of K (and of V), and a thread's share */
     static constexpr int UNITS = PCfg<D>::TILE * D * 2 / 16;
     static constexpr int UPT = UNITS / (PCfg<D>::W * 64);
@@ -198,6 +204,7 @@ struct PBlock {
     bool rok;                  /* the lane's row exists */
     uint32_t rj, rh;           /* its token and query head */
     uint32_t rlo, rhi;         /* the positions it sees */
+    uint32_t col0;             /* the wave's first output column */
 };
 
 template <int D>
@@ -250,7 +257,8 @@ __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
     }
     P.head_row = (size_t)kvh * sq.cap;
 
-    const uint32_t r = r0 + kPRows * w + l32;
+    const uint32_t r = r0 + kPRows * (w / PCfg<D>::CS) + l32;
+    P.col0 = (w % PCfg<D>::CS) * PCfg<D>::OC;
     P.rok = r < R;
     P.rj = (P.rok ? r : r0) / G;
     P.rh = kvh * G + (P.rok ? r : r0) % G;
@@ -260,7 +268,8 @@ __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
 }
 
 /* the lane's query row in f16, scaled by the score scale times log2(e):
-   the B operands of the score product */
+   the B operands of the score product (the wave's columns P.col0 .. when
+   the row is split) */
 template <int D>
 __device__ __forceinline__ void load_query(const PrefillArgs &A, const PBlock &P,
                                            h8 *qb)
@@ -269,8 +278,8 @@ __device__ __forceinline__ void load_query(const PrefillArgs &A, const PBlock &P
     const float *qrow = P.sq->q + ((size_t)P.rj * A.n_head + P.rh) * hd;
     const float f = A.scale * kLog2e;
 #pragma unroll
-    for (int s = 0; s < D / 16; s++) {
-        const uint32_t c = 16 * s + 8 * g;
+    for (int s = 0; s < D / 16 / PCfg<D>::CS; s++) {
+        const uint32_t c = P.col0 + 16 * s + 8 * g;
         const bool cok = P.rok && c < hd;
         const float4 x0 = *(const float4 *)(qrow + (cok ? c : 0));
         const float4 x1 = *(const float4 *)(qrow + (cok ? c + 4 : 0));
@@ -289,23 +298,28 @@ __device__ __forceinline__ void load_query(const PrefillArgs &A, const PBlock &P
  * of value k-step ks for columns 32 c .. 32 c + 31 (positions 16 ks +
  * 4 (l / 32) + 0..3 and + 8 of column 32 c + l % 32).
  */
-template <int D, bool PIPE, class KOp, class VOp>
+struct NoExchange {
+    template <class T> __device__ void operator()(T *) const {}
+};
+
+template <int D, bool PIPE, class KOp, class VOp, class XOp = NoExchange>
 __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8 *qb,
                                           float &m, float &lsum, f16x *o,
-                                          KOp kop, VOp vop)
+                                          KOp kop, VOp vop, XOp xop = XOp())
 {
     constexpr int kNPB = PCfg<D>::NPB, kTile = PCfg<D>::TILE;
-    constexpr int KS = D / 16, CT = D / 32;
+    constexpr int KS = D / 16 / PCfg<D>::CS, CT = PCfg<D>::OC / 32;
     const uint32_t g = (threadIdx.x & 63) >> 5;
     /* scores less the row's maximum so far (the accumulators start at
-       -m): kNPB blocks of 32 positions */
+       -m; a split row's second half starts at 0): kNPB blocks of 32
+       positions */
     const float mref = m == -INFINITY ? 0.0f : m;
     f16x sacc[kNPB];
 #pragma unroll
     for (int b = 0; b < kNPB; b++)
 #pragma unroll
         for (int i = 0; i < 16; i++)
-            sacc[b][i] = -mref;
+            sacc[b][i] = P.col0 == 0 ? -mref : 0.0f;
     /* PIPE: the operands of k-step s + 1 are asked for before the products
        of step s, so the LDS latency hides behind them (32 more registers) */
     if constexpr (!PIPE) {
@@ -339,6 +353,10 @@ __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8
         __builtin_amdgcn_sched_group_barrier(0x008, kNPB, 0);
     }
     }
+
+    /* a split row: the two partial scores summed (the same sum in both
+       waves) */
+    xop(sacc);
 
     /* masks, only where a row of the wave sees part of the tile */
     const bool partial = !(P.rlo <= p0 && P.rhi >= p0 + kTile - 1);
@@ -396,8 +414,9 @@ __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8
     }
     lsum += ls;
 
-    /* O^T += V^T . P^T (PIPE: operands one k-step ahead) */
-    if constexpr (!PIPE) {
+    /* O^T += V^T . P^T (PIPE: operands one k-step ahead, except at head
+       size 512, whose 8 column tiles of read-ahead would not fit) */
+    if constexpr (!PIPE || D > 256) {
 #pragma unroll
         for (int ks = 0; ks < 2 * kNPB; ks++)
 #pragma unroll
@@ -441,10 +460,10 @@ __device__ __forceinline__ void write_out(const PrefillArgs &A, const PBlock &P,
     const float inv = 1.0f / lt;
     const size_t obase = ((size_t)P.rj * A.n_head + P.rh) * hd;
 #pragma unroll
-    for (int c = 0; c < D / 32; c++)
+    for (int c = 0; c < PCfg<D>::OC / 32; c++)
 #pragma unroll
         for (int q4 = 0; q4 < 4; q4++) {
-            const uint32_t col = 32 * c + 8 * q4 + 4 * g;
+            const uint32_t col = P.col0 + 32 * c + 8 * q4 + 4 * g;
             if (col >= hd)
                 continue;
             float x[4];
@@ -477,14 +496,14 @@ __device__ __forceinline__ void finish(const PrefillArgs &A, const PBlock &P,
     if (!P.rok)
         return;
     const size_t pr = P.sq->part0 + ((size_t)P.rj * A.n_head + P.rh) * P.nseg + P.seg;
-    if (g == 0)
+    if (g == 0 && P.col0 == 0)
         *(float2 *)(A.part_ml + 2 * pr) = float2{m, lt};
     float *dst = A.part_acc + pr * hd;
 #pragma unroll
-    for (int c = 0; c < D / 32; c++)
+    for (int c = 0; c < PCfg<D>::OC / 32; c++)
 #pragma unroll
         for (int q4 = 0; q4 < 4; q4++) {
-            const uint32_t col = 32 * c + 8 * q4 + 4 * g;
+            const uint32_t col = P.col0 + 32 * c + 8 * q4 + 4 * g;
             if (col < hd)
                 *(float4 *)(dst + col) = float4{o[c][4 * q4], o[c][4 * q4 + 1],
                                                 o[c][4 * q4 + 2], o[c][4 * q4 + 3]};
@@ -518,6 +537,9 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_kernel(const PrefillA
     static_assert(S::UPT >= 1 && S::UNITS % (kPWaves * 64) == 0, "tile loads");
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][kTile][S::KP];
     __shared__ __attribute__((aligned(16))) _Float16 sV[2][kTile][S::VP];
+    /* the partial scores of split rows, a wave's 64 lanes x 16 x kNPB */
+    constexpr int kCS = PCfg<D>::CS;
+    __shared__ __attribute__((aligned(16))) float sX[kCS > 1 ? kPWaves : 1][64][16 * PCfg<D>::NPB];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t g = lane >> 5, l32 = lane & 31, l16 = lane & 15;
@@ -577,17 +599,42 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_kernel(const PrefillA
         const int buf = (tile - P.tfirst) & 1;
         if (tile < P.tlast)
             load(tile + 1, kr, vr, kz, vz);
-        tile_pass<D, false>(
+        tile_pass<D, (D > 256)>(
             tile * kTile, P, qb, m, lsum, o,
             [&](int s, int b) {
-                return *(const h8 *)&sK[buf][32 * b + l32][16 * s + 8 * g];
+                return *(const h8 *)&sK[buf][32 * b + l32][P.col0 + 16 * s + 8 * g];
             },
             [&](int ks, int c) {
                 const uint32_t tr = 16 * ks + 4 * g + (l16 >> 2);
-                const uint32_t tc = 32 * c + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
+                const uint32_t tc = P.col0 + 32 * c + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
                 const h4 x = lds_read_tr(&sV[buf][tr][tc]);
                 const h4 y = lds_read_tr(&sV[buf][tr + 8][tc]);
                 return h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+            },
+            [&](f16x *sacc) {
+                if constexpr (kCS > 1) {
+                    const uint32_t w = tid >> 6;
+#pragma unroll
+                    for (int b = 0; b < PCfg<D>::NPB; b++)
+#pragma unroll
+                        for (int i = 0; i < 16; i += 4)
+                            *(float4 *)&sX[w][lane][16 * b + i] =
+                                float4{sacc[b][i], sacc[b][i + 1], sacc[b][i + 2], sacc[b][i + 3]};
+                    __syncthreads();
+#pragma unroll
+                    for (int b = 0; b < PCfg<D>::NPB; b++)
+#pragma unroll
+                        for (int i = 0; i < 16; i += 4) {
+                            const float4 x = *(const float4 *)&sX[w ^ 1][lane][16 * b + i];
+                            /* half 0's partial first, in both waves */
+                            const bool h0 = P.col0 == 0;
+                            sacc[b][i] = h0 ? sacc[b][i] + x.x : x.x + sacc[b][i];
+                            sacc[b][i + 1] = h0 ? sacc[b][i + 1] + x.y : x.y + sacc[b][i + 1];
+                            sacc[b][i + 2] = h0 ? sacc[b][i + 2] + x.z : x.z + sacc[b][i + 2];
+                            sacc[b][i + 3] = h0 ? sacc[b][i + 3] + x.w : x.w + sacc[b][i + 3];
+                        }
+                    /* the next tile's writes come after its barriers */
+                }
             });
         if (tile < P.tlast) {
             __syncthreads(); /* every wave is done with the other buffer */
@@ -761,38 +808,38 @@ __global__ __launch_bounds__(kPMergeRows * 64) void pmerge_kernel(const PrefillA
     float mx = -INFINITY;
     for (uint32_t s = 0; s < nseg; s++)
         mx = fmaxf(mx, A.part_ml[2 * (pr0 + s)]);
-    const uint32_t col = 4 * lane;
-    if (col >= hd)
-        return;
-    float l = 0.0f;
-    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t s = 0; s < nseg; s++) {
-        const float2 ml = *(const float2 *)(A.part_ml + 2 * (pr0 + s));
-        const float wt = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - mx);
-        const float4 v = *(const float4 *)(A.part_acc + (pr0 + s) * hd + col);
-        l += wt * ml.y;
-        acc.x += wt * v.x;
-        acc.y += wt * v.y;
-        acc.z += wt * v.z;
-        acc.w += wt * v.w;
-    }
-    const float inv = 1.0f / l;
-    const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
-    float x[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+    /* lane t: columns 4 t .. 4 t + 3, then 256 further (head size 512) */
+    for (uint32_t col = 4 * lane; col < hd; col += 256) {
+        float l = 0.0f;
+        float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t s = 0; s < nseg; s++) {
+            const float2 ml = *(const float2 *)(A.part_ml + 2 * (pr0 + s));
+            const float wt = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - mx);
+            const float4 v = *(const float4 *)(A.part_acc + (pr0 + s) * hd + col);
+            l += wt * ml.y;
+            acc.x += wt * v.x;
+            acc.y += wt * v.y;
+            acc.z += wt * v.z;
+            acc.w += wt * v.w;
+        }
+        const float inv = 1.0f / l;
+        const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
+        float x[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        if (A.gate_mode == kGateElem)
-            x[e] *= 1.0f / (1.0f + expf(-sq.gate[oi + e]));
-        else if (A.gate_mode == kGateHead)
-            x[e] *= 1.0f / (1.0f + expf(-sq.gate[(size_t)j * A.n_head + h]));
+        for (int e = 0; e < 4; e++) {
+            if (A.gate_mode == kGateElem)
+                x[e] *= 1.0f / (1.0f + expf(-sq.gate[oi + e]));
+            else if (A.gate_mode == kGateHead)
+                x[e] *= 1.0f / (1.0f + expf(-sq.gate[(size_t)j * A.n_head + h]));
+        }
+        *(float4 *)(sq.out + oi) = float4{x[0], x[1], x[2], x[3]};
     }
-    *(float4 *)(sq.out + oi) = float4{x[0], x[1], x[2], x[3]};
 }
 
 template <int T, int D>
 hipError_t launch_d(const PrefillArgs &a, hipStream_t s)
 {
-    if constexpr (T == kF16 && D >= 128)
+    if constexpr (T == kF16 && (D == 128 || D == 256))
         hipLaunchKernelGGL((prefill_dma_kernel<D>), dim3(a.n_wg), dim3(PCfg<D>::W * 64), 0, s, a);
     else
         hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(a.n_wg), dim3(PCfg<D>::W * 64), 0, s, a);
@@ -808,6 +855,8 @@ hipError_t launch_t(const PrefillArgs &a, hipStream_t s)
         return launch_d<T, 128>(a, s);
     if (a.hd <= 256)
         return launch_d<T, 256>(a, s);
+    if (a.hd <= 512)
+        return launch_d<T, 512>(a, s);
     return hipErrorInvalidValue;
 }
 
@@ -816,12 +865,12 @@ hipError_t launch_t(const PrefillArgs &a, hipStream_t s)
 int prefill_supported(int kv, uint32_t hd)
 {
     return (kv == kF16 || kv == kI8 || kv == kI16) && hd >= 8 && hd % 8 == 0 &&
-           hd <= 256;
+           hd <= 512;
 }
 
 uint32_t prefill_tile(uint32_t hd)
 {
-    return hd > 128 ? PCfg<256>::TILE : PCfg<128>::TILE;
+    return hd > 256 ? PCfg<512>::TILE : hd > 128 ? PCfg<256>::TILE : PCfg<128>::TILE;
 }
 
 hipError_t launch_prefill_merge(const PrefillArgs &a, uint32_t n_wg, hipStream_t s)
@@ -833,7 +882,8 @@ hipError_t launch_prefill_merge(const PrefillArgs &a, uint32_t n_wg, hipStream_t
 uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd)
 {
     /* a workgroup takes PCfg::BLOCK of a KV head's n x group rows */
-    const uint64_t block = hd > 128 ? PCfg<256>::BLOCK : PCfg<128>::BLOCK;
+    const uint64_t block = hd > 256 ? PCfg<512>::BLOCK
+                         : hd > 128 ? PCfg<256>::BLOCK : PCfg<128>::BLOCK;
     return (uint32_t)(((uint64_t)n * group + block - 1) / block);
 }
 

@@ -16,8 +16,8 @@ import pytest
 import torch
 
 import janas_amd
-from attn_helpers import (KV_F16, TOL_F16_ABS, abs_err, cache, config,
-                          oracle_out, threads)
+from attn_helpers import (KV_F16, KV_F32, TOL_F16_ABS, TOL_F32_REL, abs_err,
+                          cache, config, oracle_out, rel_err, threads)
 from cases import normal
 from janas_amd import Attention
 from oracle import orc
@@ -129,6 +129,12 @@ SHAPES = {
     "g8_hd256_cfg4": (16, 2, 256, 1100, 700, 300, 0, 1.0 / 16),
     "g4_hd256_window": (8, 2, 256, 900, 257, 600, 300, None),
     "g3_hd200": (6, 2, 200, 500, 130, 100, 0, None),
+    # head size 512 (Gemma 4's global layers): each row split into two
+    # column halves whose partial scores meet in LDS; 384 and 264 leave the
+    # second half partly or almost wholly past the row
+    "g8_hd512_scale": (16, 2, 512, 900, 300, 400, 0, 0.02),
+    "g4_hd384_window": (8, 2, 384, 800, 200, 500, 256, None),
+    "g2_hd264": (4, 2, 264, 500, 130, 100, 0, None),
 }
 
 
@@ -235,6 +241,7 @@ SPLITS = {
     "hd128_g8_n100": (16, 2, 128, 5000, 100, 4800, 0),
     "hd96_window": (8, 2, 96, 4000, 90, 3500, 2000),
     "hd256_n100": (16, 2, 256, 2200, 100, 2000, 0),
+    "hd512_n80": (8, 2, 512, 2100, 80, 2000, 0),
     # from position 0: the first row block has one tile for two segments
     # (an empty segment, merged as no weight)
     "hd64_n1536_start": (8, 2, 64, 1600, 1536, 0, 0),
@@ -282,7 +289,9 @@ def quantized(seed, n_kv, cap, hd, wide):
                                        n=200, pos0=600, window=200,
                                        ring=True),
                                   dict(n_head=16, n_kv=2, hd=256, cap=800,
-                                       n=500, pos0=100)])
+                                       n=500, pos0=100),
+                                  dict(n_head=16, n_kv=2, hd=512, cap=900,
+                                       n=300, pos0=400, window=1024)])
 def test_prefill_quantized_cache(gpu, wide, geom):
     """int8 / int16 caches with their scales (the engine's own format) on
     the MFMA path: rows dequantized into f16 as tiles are staged; the bar is
@@ -315,19 +324,23 @@ def test_prefill_quantized_cache(gpu, wide, geom):
 
 
 def test_prefill_refuses_what_it_has_no_kernel_for(gpu):
-    """f32 caches and head sizes above 256 have no prefill kernel:
-    janas_attn_run_dev_prefill says ENOTSUP, janas_attn_run_dev takes the
-    split path."""
-    h, kvh, hd, cap, n = 4, 2, 512, 300, 100
-    s = dict(k=cache(301, kvh, cap, hd, np.float16),
-             v=cache(302, kvh, cap, hd, np.float16),
-             q=normal(303, n * h * hd).reshape(n, h, hd), pos0=0, n=n)
+    """f32 caches have no prefill kernel: janas_attn_run_dev_prefill says
+    ENOTSUP, janas_attn_run_dev takes the split path (float-accurate)."""
+    h, kvh, hd, cap, n = 4, 2, 128, 300, 100
+    k = cache(301, kvh, cap, hd, np.float32)
+    v = cache(302, kvh, cap, hd, np.float32)
+    q = normal(303, n * h * hd).reshape(n, h, hd)
+    d = dict(k=to_dev(k, gpu), v=to_dev(v, gpu), q=to_dev(q, gpu),
+             out=torch.full((n, h, hd), float("nan"), device=gpu),
+             cap=cap, n=n, pos0=0)
     with Attention(h, kvh, hd, cap) as a:
         with pytest.raises(janas_amd.AttnError) as e:
-            run_prefill(a, [s], gpu)
+            a.run_dev(KV_F32, [d], path="prefill")
         assert e.value.code == -5
         a.prof_enable(True)
-        (out,) = run_prefill(a, [s], gpu, path="auto")
+        a.run_dev(KV_F32, [d], path="auto")
+        torch.cuda.synchronize()
         assert prefill_launches(a) == 0
-    err = abs_err(out, oracle(dict(n_head=h, n_kv=kvh, hd=hd), s))
-    assert err <= TOL_F16_ABS
+    ref = orc.run(q, k, v, None, None, n_head=h, n_kv=kvh, hd=hd, pos0=0,
+                  kv=KV_F32, threads=threads(), block=64)
+    assert rel_err(d["out"].cpu().numpy(), ref) <= TOL_F32_REL
