@@ -177,8 +177,8 @@ int janas_attn_run_dev_split(struct janas_attn *a, int kv_type, int gate_mode,
 
 /* The same, always through the MFMA prefill path: f16, int8 and int16
    caches (the latter two dequantized into f16 as tiles are staged),
-   head_dim up to 256 (JANAS_ATTN_ENOTSUP otherwise - f32 caches, larger
-   heads; janas_attn_run_dev then takes the split-KV path). */
+   head_dim up to 512 (JANAS_ATTN_ENOTSUP for f32 caches;
+   janas_attn_run_dev then takes the split-KV path). */
 int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
                                int gate_mode,
                                const struct janas_attn_seq *seqs,

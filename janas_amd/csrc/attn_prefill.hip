@@ -13,9 +13,11 @@
  *   workgroup   8 waves, 256 query rows = 64 tokens x the 4 (or G) query
  *               heads of one KV head, so each K/V tile is read once for the
  *               whole GQA group (head size 256: 4 waves, 128 rows, one wave
- *               a SIMD with 512 registers, and 64-position key tiles). Row blocks of later tokens (more keys to
- *               see) are dispatched first; consecutive workgroups share a KV
- *               head, so they share an XCD's L2.
+ *               a SIMD with 512 registers, and 64-position key tiles; head
+ *               size 512: 4 waves as 2 row groups x 2 column halves, 64
+ *               rows, 32-position tiles). Row blocks of later tokens (more
+ *               keys to see) are dispatched first; consecutive workgroups
+ *               share a KV head, so they share an XCD's L2.
  *   key tiles   128 positions of K and V in LDS, two buffers; the next
  *               tile is loaded while this one is computed. 128 rather than
  *               64 positions: the tile's fixed costs (barriers, the row
