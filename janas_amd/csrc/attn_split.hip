@@ -102,7 +102,11 @@ template <int T, int D> struct Shape {
     static constexpr int VRB = T == kI8 ? 2 * RB : RB; /* bytes of a V row in LDS */
 };
 
-template <int T, int D, bool NT>
+/* ONE: a launch of one sequence - its descriptor is read at fixed offsets
+   with the rest of the arguments, not after the launch's sequence count (a
+   round trip to the arguments earlier for the first loads, 0.4 us a
+   decode) */
+template <int T, int D, bool NT, bool ONE = false>
 __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
 {
     using E = Elem<T>;
@@ -120,8 +124,9 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
     const uint32_t g16 = lane >> 4, l16 = lane & 15;
     const uint32_t id = xcd_remap(blockIdx.x, gridDim.x);
     uint32_t si = 0;
-    while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
-        si++;
+    if constexpr (!ONE)
+        while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
+            si++;
     const SeqDesc &sq = A.seq[si];
     const uint32_t G = A.group, hd = A.hd;
     const uint32_t local = id - sq.wg0;
@@ -514,7 +519,7 @@ __device__ __forceinline__ float &f4e(float4 &v, int e)
  * enough to fill the GPU with 4 times fewer workgroups (blocks of tokens),
  * 1 when it has few (a decode spreads its loads over more CUs).
  */
-template <int CPL>
+template <int CPL, bool ONE = false>
 __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 {
     constexpr uint32_t kCols = kMergeLanes * CPL;
@@ -523,8 +528,9 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     const uint32_t id = blockIdx.x, tid = threadIdx.x;
     const uint32_t g = tid / kMergeLanes, cl = tid % kMergeLanes;
     uint32_t si = 0;
-    while (si + 1 < A.n_seqs && A.seq[si + 1].mg0 <= id)
-        si++;
+    if constexpr (!ONE)
+        while (si + 1 < A.n_seqs && A.seq[si + 1].mg0 <= id)
+            si++;
     const SeqDesc &sq = A.seq[si];
     const uint32_t hd = A.hd, G = A.group, nd = (hd + kCols - 1) / kCols;
     const uint32_t local = id - sq.mg0, db = local % nd;
@@ -639,7 +645,9 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 template <int T, int D>
 hipError_t launch_t(const SplitArgs &a, hipStream_t s)
 {
-    if (a.once)
+    if (a.once && a.n_seqs == 1)
+        hipLaunchKernelGGL((split_kernel<T, D, true, true>), dim3(a.n_wg), dim3(512), 0, s, a);
+    else if (a.once)
         hipLaunchKernelGGL((split_kernel<T, D, true>), dim3(a.n_wg), dim3(512), 0, s, a);
     else
         hipLaunchKernelGGL((split_kernel<T, D, false>), dim3(a.n_wg), dim3(512), 0, s, a);
@@ -694,8 +702,13 @@ uint32_t merge_cols(uint64_t pairs, uint32_t hd)
 
 hipError_t launch_merge(const SplitArgs &a, uint32_t n_wg, hipStream_t s)
 {
-    if (a.merge_cols == 128)
+    const bool one = a.n_seqs == 1;
+    if (a.merge_cols == 128 && one)
+        hipLaunchKernelGGL((merge_kernel<4, true>), dim3(n_wg), dim3(256), 0, s, a);
+    else if (a.merge_cols == 128)
         hipLaunchKernelGGL(merge_kernel<4>, dim3(n_wg), dim3(256), 0, s, a);
+    else if (a.merge_cols == 32 && one)
+        hipLaunchKernelGGL((merge_kernel<1, true>), dim3(n_wg), dim3(256), 0, s, a);
     else if (a.merge_cols == 32)
         hipLaunchKernelGGL(merge_kernel<1>, dim3(n_wg), dim3(256), 0, s, a);
     else

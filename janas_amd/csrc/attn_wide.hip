@@ -91,7 +91,8 @@ template <int T, int D> struct WShape {
     static constexpr int REGION = kRound * VB / 1024 * kBlk;
 };
 
-template <int T, int D, int NB>
+/* ONE: a launch of one sequence, its descriptor read at fixed offsets */
+template <int T, int D, int NB, bool ONE = false>
 __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 {
     using E = Elem<T>;
@@ -112,8 +113,9 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     const uint32_t g16 = lane >> 4, l16 = lane & 15;
     const uint32_t id = xcd_remap(blockIdx.x, gridDim.x);
     uint32_t si = 0;
-    while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
-        si++;
+    if constexpr (!ONE)
+        while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
+            si++;
     const SeqDesc &sq = A.seq[si];
     const uint32_t G = A.group, hd = A.hd;
     const uint32_t local = id - sq.wg0;
@@ -467,7 +469,10 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 template <int T, int D, int NB>
 hipError_t launch_w(const SplitArgs &a, hipStream_t s)
 {
-    hipLaunchKernelGGL((wide_kernel<T, D, NB>), dim3(a.n_wg), dim3(256), 0, s, a);
+    if (a.n_seqs == 1)
+        hipLaunchKernelGGL((wide_kernel<T, D, NB, true>), dim3(a.n_wg), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((wide_kernel<T, D, NB>), dim3(a.n_wg), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
