@@ -154,8 +154,12 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t n)
     /* blocks are dealt to the 8 XCDs round robin: give each XCD a
        contiguous run of logical ids, so that the row tiles of one chunk
        (consecutive ids) share an L2 */
-    uint32_t x = bid % 8, k = bid / 8, q = n / 8, r = n % 8;
-    return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
+    /* XCD x (of 8) holds ids x q + min(x, r) .. : n = 8 q + r, the first r
+       XCDs one more; branch-free, so the argument loads after it are not
+       split across branches. n comes from the arguments (n_wg), loaded with
+       the rest, not from the dispatch's grid size */
+    const uint32_t x = bid % 8, k = bid / 8, q = n / 8, r = n % 8;
+    return x * q + (x < r ? x : r) + k;
 }
 
 constexpr int kBlk = 1024 + 32;  /* LDS bytes of a kilobyte of rows */

@@ -122,13 +122,17 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t g16 = lane >> 4, l16 = lane & 15;
-    const uint32_t id = xcd_remap(blockIdx.x, gridDim.x);
+    const uint32_t id = xcd_remap(blockIdx.x, A.n_wg);
     uint32_t si = 0;
     if constexpr (!ONE)
         while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
             si++;
     const SeqDesc &sq = A.seq[si];
     const uint32_t G = A.group, hd = A.hd;
+    /* the cache and query addresses with the first batch of argument loads
+       (otherwise the compiler asks for them just before the big loads, one
+       round trip later) */
+    asm volatile("" ::"s"(sq.k), "s"(sq.v), "s"(sq.q), "s"(A.n_head));
     const uint32_t local = id - sq.wg0;
     const uint32_t rt = local % sq.rtiles;
     const uint32_t c = sq.c0 + (local / sq.rtiles) % sq.span;
@@ -545,20 +549,20 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
        are inside the row or none is) */
     const uint32_t col = db * kCols + CPL * cl;
     const bool colok = col < hd;
-    /* the gate, asked for before the partials so the two loads overlap */
+    /* the gate, asked for with the partials so the loads overlap: branch-
+       free (a load under a branch is waited for where the branches join,
+       before the partials' loads), from a valid dummy address when unused */
     const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
+    const bool gel = A.gate_mode == kGateElem && colok;
+    const float *gsrc = gel ? sq.gate + oi : A.part_ml;
+    const float *hsrc = A.gate_mode == kGateHead ? sq.gate + (size_t)j * A.n_head + h
+                                                 : A.part_ml;
     float4 gv = {0.0f, 0.0f, 0.0f, 0.0f};
-    float gh = 0.0f;
-    if (g == 0 && colok) {
-        if (A.gate_mode == kGateElem) {
-            if constexpr (CPL == 4)
-                gv = *(const float4 *)(sq.gate + oi);
-            else
-                gv.x = sq.gate[oi];
-        } else if (A.gate_mode == kGateHead) {
-            gh = sq.gate[(size_t)j * A.n_head + h];
-        }
-    }
+    if constexpr (CPL == 4)
+        gv = *(const float4 *)gsrc;
+    else
+        gv.x = *gsrc;
+    const float gh = *hsrc;
     float mg = -INFINITY, lg = 0.0f;
     float4 ag = {0.0f, 0.0f, 0.0f, 0.0f};
     for (uint32_t i0 = g; i0 < nc; i0 += kMergeGroups * kMergeBatch) {

@@ -111,13 +111,15 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t g16 = lane >> 4, l16 = lane & 15;
-    const uint32_t id = xcd_remap(blockIdx.x, gridDim.x);
+    const uint32_t id = xcd_remap(blockIdx.x, A.n_wg);
     uint32_t si = 0;
     if constexpr (!ONE)
         while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
             si++;
     const SeqDesc &sq = A.seq[si];
     const uint32_t G = A.group, hd = A.hd;
+    /* the cache and query addresses with the first batch of argument loads */
+    asm volatile("" ::"s"(sq.k), "s"(sq.v), "s"(sq.q), "s"(A.n_head));
     const uint32_t local = id - sq.wg0;
     const uint32_t rt = local % sq.rtiles;
     const uint32_t c = sq.c0 + (local / sq.rtiles) % sq.span;
