@@ -189,14 +189,20 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
         }
     }
     /* K and V: byte 1024 i + 16 lane of the wave's 32 rows */
+    /* the chunk's rows start at one address per block; a lane's byte
+       offset from it stays below kChunk rows, 32 bits (the loads take the
+       base in scalar registers and the offset in one vector register) */
     u4 kraw[S::UNITS], vraw[S::UNITS];
-    size_t off[S::UNITS];
+    const uint32_t rbytes = hd * S::EB, rlast = plast - t0;
+    const char *const kbase = (const char *)sq.k + crow * rbytes;
+    const char *const vbase = (const char *)sq.v + crow * rbytes;
+    uint32_t off[S::UNITS];
     bool back[S::UNITS]; /* int8 rows of 8 mod 16 bytes: unit_at() */
 #pragma unroll
     for (int i = 0; i < S::UNITS; i++) {
         const uint32_t byte = i * 1024 + lane * 16;
         const uint32_t row = byte / S::RB, cb = byte % S::RB;
-        const uint32_t p = p0w + row;
+        const uint32_t p = w * kWavePos + row; /* from t0 */
         uint32_t at;
         if constexpr (S::EB == 1) {
             at = unit_at(cb, hd, back[i]);
@@ -204,18 +210,18 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
             at = cb < hd * S::EB ? cb : 0;
             back[i] = false;
         }
-        off[i] = (crow + ((p < plast ? p : plast) - t0)) * (hd * S::EB) + at;
+        off[i] = __umul24(p < rlast ? p : rlast, rbytes) + at;
     }
     /* NT: every chunk is read by one row tile (decode), once: nontemporal;
        one that several row tiles read (blocks of tokens) should stay in L2 */
     if constexpr (NT) {
 #pragma unroll
         for (int i = 0; i < S::UNITS; i++)
-            kraw[i] = __builtin_nontemporal_load((const u4 *)((const char *)sq.k + off[i]));
+            kraw[i] = __builtin_nontemporal_load((const u4 *)(kbase + off[i]));
     } else {
 #pragma unroll
         for (int i = 0; i < S::UNITS; i++)
-            kraw[i] = *(const u4 *)((const char *)sq.k + off[i]);
+            kraw[i] = *(const u4 *)(kbase + off[i]);
     }
     /* the scales of the lane's positions 16 mt + 4 g16 + i */
     float ks8[8], vs8[8];
@@ -227,10 +233,10 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
     if constexpr (S::SCALED) {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const uint32_t p = p0w + 16 * (e / 4) + 4 * g16 + e % 4;
-            const size_t at = crow + ((p < plast ? p : plast) - t0);
-            ks8[e] = sq.ks[at];
-            vs8[e] = sq.vs[at];
+            const uint32_t p = w * kWavePos + 16 * (e / 4) + 4 * g16 + e % 4;
+            const uint32_t at = p < rlast ? p : rlast;
+            ks8[e] = sq.ks[crow + at];
+            vs8[e] = sq.vs[crow + at];
         }
     }
 
@@ -282,11 +288,11 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
     if constexpr (NT) {
 #pragma unroll
         for (int i = 0; i < S::UNITS; i++)
-            vraw[i] = __builtin_nontemporal_load((const u4 *)((const char *)sq.v + off[i]));
+            vraw[i] = __builtin_nontemporal_load((const u4 *)(vbase + off[i]));
     } else {
 #pragma unroll
         for (int i = 0; i < S::UNITS; i++)
-            vraw[i] = *(const u4 *)((const char *)sq.v + off[i]);
+            vraw[i] = *(const u4 *)(vbase + off[i]);
     }
     f4 sacc[2];
     {

@@ -142,7 +142,12 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     /* rows of the chunk in the cache: contiguous, a ring's too (cap is a
        multiple of the chunk) */
     const size_t crow = (size_t)kvh * sq.cap + (A.ring ? t0 % sq.cap : t0);
-    const size_t rstride = (size_t)hd * S::EB;
+    /* the chunk's rows start at one address per block; a lane's byte
+       offset from it stays below kChunk rows, 32 bits (the loads take the
+       base in scalar registers and the offset in one vector register) */
+    const uint32_t rbytes = hd * S::EB, rlast = plast - t0;
+    const char *const kbase = (const char *)sq.k + crow * rbytes;
+    const char *const vbase = (const char *)sq.v + crow * rbytes;
 
     if (tid < kRows) {
         uint32_t r = r0 + tid;
@@ -177,15 +182,14 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     /* the scales of the chunk's positions, one a thread */
     float kz = 1.0f, vz = 1.0f;
     if constexpr (S::SCALED) {
-        const uint32_t p = t0 + tid;
-        const size_t at = crow + ((p < plast ? p : plast) - t0);
-        kz = sq.ks[at];
-        vz = sq.vs[at];
+        const uint32_t at = tid < rlast ? tid : rlast;
+        kz = sq.ks[crow + at];
+        vz = sq.vs[crow + at];
     }
     /* round s (K 0..3, V 0..3): byte 1024 i + 16 lane of its 16 rows */
     auto load_round = [&](u4 *buf, int s) {
-        const char *base = (const char *)(s < kRounds ? sq.k : sq.v);
-        const uint32_t p0 = p0w + kRound * (s % kRounds);
+        const char *base = s < kRounds ? kbase : vbase;
+        const uint32_t p0 = w * kWPos + kRound * (s % kRounds); /* from t0 */
 #pragma unroll
         for (int i = 0; i < S::UNITS; i++) {
             const uint32_t byte = i * 1024 + lane * 16;
@@ -198,7 +202,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
             } else {
                 at = cb < hd * S::EB ? cb : 0;
             }
-            const size_t off = (crow + ((p < plast ? p : plast) - t0)) * rstride + at;
+            const uint32_t off = __umul24(p < rlast ? p : rlast, rbytes) + at;
             buf[i] = __builtin_nontemporal_load((const u4 *)(base + off));
         }
     };
