@@ -714,19 +714,27 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
     /* held in registers: read through P.sq inside the loop they would be
        reloaded after every load into LDS, and a pending scalar load makes
        each LDS operand wait drain the whole queue */
-    const uint16_t *const kg = (const uint16_t *)sq.k, *const vg = (const uint16_t *)sq.v;
-    const uint32_t cap = sq.cap;
+    const char *const kg = (const char *)sq.k, *const vg = (const char *)sq.v;
+    const uint32_t cap = sq.cap, rbytes = hd * 2;
+    const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
+    /* a tile's rows are contiguous in the cache (a ring's capacity is a
+       multiple of 256 positions): one base a tile, in scalar registers, and
+       a 32-bit offset a lane. Rows outside the block's positions read the
+       nearest one inside [lo_all, hi_all], which lies in the same tile */
     auto fetch = [&](uint32_t tile, char *dk, char *dv) {
+        const uint32_t t0 = tile * kTile;
+        const size_t base = (P.head_row + (ring ? t0 % cap : t0)) * rbytes;
 #pragma unroll
         for (int j = 0; j < (int)NJ; j++) {
-            const size_t cr = cache_row(P, cap, ring, tile * kTile + drow + RPI * kW * j);
-            const size_t off = cr * hd + dcol[j];
-            const uint32_t at = (w + kW * j) * 1024;
+            uint32_t p = t0 + drow + RPI * kW * j;
+            p = p < P.lo_all ? P.lo_all : p > P.hi_all ? P.hi_all : p;
+            const uint32_t off = __umul24(p - t0, rbytes) + 2 * dcol[j];
+            const uint32_t at = (wu + kW * j) * 1024;
             __builtin_amdgcn_global_load_lds(
-                (const void *)(kg + off),
+                (const void *)(kg + base + off),
                 (__attribute__((address_space(3))) void *)(dk + at), 16, 0, 0);
             __builtin_amdgcn_global_load_lds(
-                (const void *)(vg + off),
+                (const void *)(vg + base + off),
                 (__attribute__((address_space(3))) void *)(dv + at), 16, 0, 0);
         }
     };
