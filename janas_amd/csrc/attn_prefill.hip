@@ -408,9 +408,13 @@ __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8
 #pragma unroll
         for (int e = 0; e < 8; e++)
             pa[ks][e] = (_Float16)__builtin_amdgcn_exp2f(sacc[ks / 2][8 * (ks % 2) + e]);
+        /* the sum from the operand's own registers (pairs rebuilt from its
+           elements are converted a second time) */
+        const uint4 pw = __builtin_bit_cast(uint4, pa[ks]);
+        const uint32_t pws[4] = {pw.x, pw.y, pw.z, pw.w};
 #pragma unroll
-        for (int e = 0; e < 8; e += 2)
-            ls = __builtin_amdgcn_fdot2(h2{pa[ks][e], pa[ks][e + 1]},
+        for (int e = 0; e < 4; e++)
+            ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pws[e]),
                                         h2{(_Float16)1.0f, (_Float16)1.0f},
                                         ls, false);
     }
