@@ -112,7 +112,8 @@ enum janas_attn_gate {
 enum janas_attn_err {
     JANAS_ATTN_OK = 0,
     JANAS_ATTN_EINVAL = -1,  /* bad arguments */
-    JANAS_ATTN_ERANGE = -2,  /* positions past the cache, a ring too small */
+    JANAS_ATTN_ERANGE = -2,  /* positions past the cache, a ring too small,
+                                n x n_head above 2^31 - 1 */
     JANAS_ATTN_ENOMEM = -3,  /* device memory */
     JANAS_ATTN_EDEVICE = -4, /* a HIP call failed */
     JANAS_ATTN_ENOTSUP = -5  /* no kernel for this element type / size */

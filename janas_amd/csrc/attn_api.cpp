@@ -93,6 +93,9 @@ int describe(const janas_attn *a, int kv, const janas_attn_seq &s, SeqDesc &d)
         return JANAS_ATTN_EINVAL;
     if ((kv == kI8 || kv == kI16) && (!s.ks || !s.vs))
         return JANAS_ATTN_EINVAL;
+    /* the kernels count a sequence's query rows (n x heads) in 32 bits */
+    if ((uint64_t)s.n * a->n_head > 0x7FFFFFFFu)
+        return JANAS_ATTN_ERANGE;
     memset(&d, 0, sizeof d);
     d.k = s.k;
     d.v = s.v;
