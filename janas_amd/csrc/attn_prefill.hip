@@ -137,18 +137,20 @@ template <int T> struct PElem;
 template <> struct PElem<kF16> {
     typedef u4 Raw;
     static constexpr bool SCALED = false;
-    __device__ static Raw load(const void *b, size_t i)
+    static constexpr uint32_t EB = 2;
+    __device__ static Raw load(const char *b, uint32_t off)
     {
-        return *(const u4 *)((const uint16_t *)b + i);
+        return *(const u4 *)(b + off);
     }
     __device__ static u4 to_f16(const Raw &r, float) { return r; }
 };
 template <> struct PElem<kI8> {
     typedef uint2 Raw;
     static constexpr bool SCALED = true;
-    __device__ static Raw load(const void *b, size_t i)
+    static constexpr uint32_t EB = 1;
+    __device__ static Raw load(const char *b, uint32_t off)
     {
-        return *(const uint2 *)((const int8_t *)b + i);
+        return *(const uint2 *)(b + off);
     }
     __device__ static u4 to_f16(const Raw &r, float z)
     {
@@ -164,9 +166,10 @@ template <> struct PElem<kI8> {
 template <> struct PElem<kI16> {
     typedef u4 Raw;
     static constexpr bool SCALED = true;
-    __device__ static Raw load(const void *b, size_t i)
+    static constexpr uint32_t EB = 2;
+    __device__ static Raw load(const char *b, uint32_t off)
     {
-        return *(const u4 *)((const int16_t *)b + i);
+        return *(const u4 *)(b + off);
     }
     __device__ static u4 to_f16(const Raw &r, float z)
     {
@@ -516,18 +519,6 @@ __device__ __forceinline__ void finish(const PrefillArgs &A, const PBlock &P,
         }
 }
 
-/* the tile position a row of the tile reads: outside [lo_all, hi_all] the
-   nearest of the two (masked, but never a row the caller has not written),
-   a ring's row modulo its size */
-__device__ __forceinline__ size_t cache_row(const PBlock &P, uint32_t cap, bool ring,
-                                            uint32_t p)
-{
-    p = p < P.lo_all ? P.lo_all : p > P.hi_all ? P.hi_all : p;
-    if (ring)
-        p %= cap;
-    return P.head_row + p;
-}
-
 /*
  * The kernel for int8 / int16 caches (dequantized with their scales as
  * tiles are staged) and head sizes up to 64: each thread loads its units
@@ -558,20 +549,30 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_kernel(const PrefillA
 
     /* ---- a tile's K and V: thread t's units t + 512 u; columns past hd
        read column 0 (their products meet zero query columns, or are not
-       stored) ---- */
+       stored). One base row a tile and 32-bit offsets, as in the DMA
+       kernel: rows outside [lo_all, hi_all] read the nearest row inside,
+       which lies in the same tile ---- */
+    const uint32_t rbytes = hd * E::EB;
     auto load = [&](uint32_t tile, typename E::Raw *kr, typename E::Raw *vr,
                     float *kz, float *vz) {
+        const uint32_t t0 = tile * kTile;
+        const size_t brow = P.head_row + (ring ? t0 % sq.cap : t0);
+        const char *const kb = (const char *)sq.k + brow * rbytes;
+        const char *const vb = (const char *)sq.v + brow * rbytes;
 #pragma unroll
         for (int u = 0; u < S::UPT; u++) {
             const uint32_t unit = tid + u * (kPWaves * 64);
             const uint32_t row = unit / S::UPR, cu = unit % S::UPR;
-            const size_t cr = cache_row(P, sq.cap, ring, tile * kTile + row);
+            uint32_t p = t0 + row;
+            p = p < P.lo_all ? P.lo_all : p > P.hi_all ? P.hi_all : p;
+            const uint32_t rel = p - t0;
             const uint32_t col = cu * 8 < hd ? cu * 8 : 0;
-            kr[u] = E::load(sq.k, cr * hd + col);
-            vr[u] = E::load(sq.v, cr * hd + col);
+            const uint32_t off = __umul24(rel, rbytes) + col * E::EB;
+            kr[u] = E::load(kb, off);
+            vr[u] = E::load(vb, off);
             if constexpr (E::SCALED) {
-                kz[u] = sq.ks[cr];
-                vz[u] = sq.vs[cr];
+                kz[u] = sq.ks[brow + rel];
+                vz[u] = sq.vs[brow + rel];
             }
         }
     };
