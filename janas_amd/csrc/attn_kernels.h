@@ -106,6 +106,24 @@ struct Q8kArgs {
 };
 
 /* Launchers (attn_split.hip). Return hipSuccess or the launch's error. */
+/* The sequence of a launch that workgroup id belongs to: the last whose
+   first workgroup (start, wg0 or mg0) is at or below id. With several
+   sequences every start is read at once - independent argument loads
+   rather than a chain of one round trip a sequence; a launch of one reads
+   none. */
+template <class Args>
+__device__ __forceinline__ uint32_t seq_index(const Args &A, uint32_t SeqDesc::*start,
+                                              uint32_t id)
+{
+    uint32_t si = 0;
+    if (A.n_seqs <= 1)
+        return 0;
+#pragma unroll
+    for (uint32_t i = 1; i < kMaxSeqs; i++)
+        si += i < A.n_seqs && A.seq[i].*start <= id;
+    return si;
+}
+
 hipError_t launch_split(int kv, const SplitArgs &a, hipStream_t s);
 hipError_t launch_merge(const SplitArgs &a, uint32_t n_wg, hipStream_t s);
 /* columns a merge workgroup takes for a launch of pairs (token, head). */

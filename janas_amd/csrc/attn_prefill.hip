@@ -219,9 +219,7 @@ __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t l32 = lane & 31;
     const uint32_t id = xcd_remap(blockIdx.x, gridDim.x);
-    uint32_t si = 0;
-    while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
-        si++;
+    const uint32_t si = seq_index(A, &SeqDesc::wg0, id);
     PBlock P;
     P.sq = &A.seq[si];
     const SeqDesc &sq = *P.sq;
@@ -810,9 +808,7 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
 __global__ __launch_bounds__(kPMergeRows * 64) void pmerge_kernel(const PrefillArgs A)
 {
     const uint32_t id = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    uint32_t si = 0;
-    while (si + 1 < A.n_seqs && A.seq[si + 1].mg0 <= id)
-        si++;
+    const uint32_t si = seq_index(A, &SeqDesc::mg0, id);
     const SeqDesc &sq = A.seq[si];
     const uint32_t hd = A.hd, nseg = sq.nseg;
     const uint32_t row = (id - sq.mg0) * kPMergeRows + w;

@@ -125,8 +125,7 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
     const uint32_t id = xcd_remap(blockIdx.x, A.n_wg);
     uint32_t si = 0;
     if constexpr (!ONE)
-        while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
-            si++;
+        si = seq_index(A, &SeqDesc::wg0, id);
     const SeqDesc &sq = A.seq[si];
     const uint32_t G = A.group, hd = A.hd;
     /* the cache and query addresses with the first batch of argument loads
@@ -539,8 +538,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     const uint32_t g = tid / kMergeLanes, cl = tid % kMergeLanes;
     uint32_t si = 0;
     if constexpr (!ONE)
-        while (si + 1 < A.n_seqs && A.seq[si + 1].mg0 <= id)
-            si++;
+        si = seq_index(A, &SeqDesc::mg0, id);
     const SeqDesc &sq = A.seq[si];
     const uint32_t hd = A.hd, G = A.group, nd = (hd + kCols - 1) / kCols;
     const uint32_t local = id - sq.mg0, db = local % nd;

@@ -114,8 +114,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     const uint32_t id = xcd_remap(blockIdx.x, A.n_wg);
     uint32_t si = 0;
     if constexpr (!ONE)
-        while (si + 1 < A.n_seqs && A.seq[si + 1].wg0 <= id)
-            si++;
+        si = seq_index(A, &SeqDesc::wg0, id);
     const SeqDesc &sq = A.seq[si];
     const uint32_t G = A.group, hd = A.hd;
     /* the cache and query addresses with the first batch of argument loads */
