@@ -1,0 +1,125 @@
+"""Seeded random geometries through janas_attn_run_dev against the CPU
+restatement: element type, head size, GQA group, block length, position,
+window, ring and output gate drawn from a fixed counter generator, on both
+paths (split-KV for blocks of up to 64 tokens, the MFMA prefill for longer
+ones). The cases are the same on every run; each prints its draw first.
+
+Bars: the split path is float-accurate (f32 cache: max |err| / max |ref|
+1e-5; int8 / int16 / f16: 1e-5 of max(1, max |ref|), the reference's FLOAT
+bar, test_attention.c:146); the prefill path computes in f16 (2e-3 abs).
+"""
+import numpy as np
+import pytest
+import torch
+
+import janas_amd
+from attn_helpers import (KV_F16, KV_F32, KV_I8, KV_I16, TOL_F16_ABS,
+                          TOL_F32_REL, TOL_FLOAT_ABS, abs_err, cache, rel_err,
+                          threads)
+from cases import normal, splitmix
+from janas_amd import Attention
+from oracle import orc
+
+pytestmark = pytest.mark.gpu
+
+N_CASES = 24
+CHUNK = 256
+
+
+def draw(i):
+    """Case i's geometry, from 12 draws of the counter generator."""
+    z = [int(x) for x in splitmix(7100 + i, 12)]
+    prefill = i % 3 == 2
+    kinds = [KV_I8, KV_I16, KV_F16] if prefill else [KV_I8, KV_I16, KV_F16, KV_F32]
+    kv = kinds[z[0] % len(kinds)]
+    hds = [64, 96, 128] if kv == KV_F32 else [64, 96, 128, 200, 256, 320, 512]
+    hd = hds[z[1] % len(hds)]
+    group = [1, 2, 4, 8][z[2] % 4]
+    n_kv = 1 + z[3] % 3
+    n = 65 + z[4] % 300 if prefill else 1 + z[4] % 64
+    pos0 = z[5] % 3000
+    window = 0 if z[6] % 2 else 64 + z[7] % 1500
+    ring = window > 0 and z[8] % 3 == 0
+    gate = z[9] % 3  # 0 none, 1 per element, 2 per head
+    if ring:
+        # a ring of whole chunks that holds the call (attention.c:1281-1286)
+        cap = CHUNK * ((window + n) // CHUNK + 3)
+    else:
+        cap = pos0 + n + z[10] % 200
+    return dict(kv=kv, hd=hd, n_head=group * n_kv, n_kv=n_kv, n=n, pos0=pos0,
+                window=window, ring=ring, gate=gate, cap=cap,
+                path="prefill" if prefill else "split", seed=9100 + 10 * i)
+
+
+def inputs(g):
+    """K / V in the cache's element type (int8 / int16 as the engine writes
+    them: each row's largest magnitude at the top code, scale max / top),
+    q, and the gate."""
+    n_kv, cap, hd, s = g["n_kv"], g["cap"], g["hd"], g["seed"]
+    ks = vs = None
+    if g["kv"] in (KV_I8, KV_I16):
+        top = np.float32(127.0 if g["kv"] == KV_I8 else 32767.0)
+        dt = np.int8 if g["kv"] == KV_I8 else np.int16
+        out = []
+        for j in (1, 2):
+            x = cache(s + j, n_kv, cap, hd, np.float32)
+            m = np.maximum(np.abs(x).max(axis=2), np.float32(1e-20))
+            out.append((np.rint(x * (top / m)[..., None]).astype(dt),
+                        (m / top).astype(np.float32)))
+        (k, ks), (v, vs) = out
+    else:
+        dt = np.float16 if g["kv"] == KV_F16 else np.float32
+        k = cache(s + 1, n_kv, cap, hd, dt)
+        v = cache(s + 2, n_kv, cap, hd, dt)
+    q = normal(s + 3, g["n"] * g["n_head"] * hd).reshape(g["n"], g["n_head"], hd)
+    gate = None
+    if g["gate"] == 1:
+        gate = normal(s + 4, g["n"] * g["n_head"] * hd).reshape(g["n"], g["n_head"], hd)
+    elif g["gate"] == 2:
+        gate = normal(s + 4, g["n"] * g["n_head"]).reshape(g["n"], g["n_head"])
+    return k, v, ks, vs, q, gate
+
+
+def to_dev(x, gpu):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(gpu)
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_geometry(gpu, i):
+    g = draw(i)
+    print(f"case {i}: {g}", flush=True)
+    k, v, ks, vs, q, gate = inputs(g)
+    n, h, hd = g["n"], g["n_head"], g["hd"]
+    d = dict(k=to_dev(k, gpu), v=to_dev(v, gpu), q=to_dev(q, gpu),
+             out=torch.full((n, h, hd), float("nan"), device=gpu),
+             cap=g["cap"], n=n, pos0=g["pos0"])
+    if ks is not None:
+        d["ks"], d["vs"] = to_dev(ks, gpu), to_dev(vs, gpu)
+    gate_mode = 0
+    if gate is not None:
+        d["gate"] = to_dev(gate, gpu)
+        gate_mode = janas_amd.GATE_ELEM if g["gate"] == 1 else janas_amd.GATE_HEAD
+    with Attention(h, g["n_kv"], hd, g["cap"]) as a:
+        if g["window"]:
+            a.set_window(g["window"])
+        if g["ring"]:
+            a.set_ring(True)
+        a.run_dev(g["kv"], [d], gate_mode=gate_mode, path=g["path"])
+        torch.cuda.synchronize()
+    out = d["out"].cpu().numpy()
+    ref = orc.run(np.ascontiguousarray(q, np.float32), k, v, ks, vs,
+                  n_head=h, n_kv=g["n_kv"], hd=hd, pos0=g["pos0"], kv=g["kv"],
+                  window=g["window"], ring=g["ring"], threads=threads(),
+                  block=64)
+    if gate is not None:
+        orc.gate(ref, gate, per_head=g["gate"] == 2)
+    assert np.isfinite(out).all()
+    if g["path"] == "prefill":
+        err, bar = abs_err(out, ref), TOL_F16_ABS
+    elif g["kv"] == KV_F32:
+        err, bar = rel_err(out, ref), TOL_F32_REL
+    else:
+        err = abs_err(out, ref)
+        bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+    print(f"case {i}: max err {err:.2e} (bar {bar:.1e})")
+    assert err <= bar
