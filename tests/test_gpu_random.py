@@ -123,3 +123,43 @@ def test_random_geometry(gpu, i):
         bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
     print(f"case {i}: max err {err:.2e} (bar {bar:.1e})")
     assert err <= bar
+
+
+@pytest.mark.parametrize("path", ["split", "prefill"])
+def test_random_many_sequences(gpu, path):
+    """19 sequences of random lengths and offsets in one call: the library
+    launches them 16 at a time, and each workgroup finds its sequence among
+    the launch's; every sequence must equal its own restatement."""
+    h, kvh, hd = 8, 2, 128
+    z = [int(x) for x in splitmix(7300 + (path == "prefill"), 3 * 19)]
+    seqs, dev = [], []
+    for i in range(19):
+        n = 1 + z[3 * i] % 40 if path == "split" else 65 + z[3 * i] % 150
+        pos0 = z[3 * i + 1] % 1500
+        cap = pos0 + n + z[3 * i + 2] % 100
+        s = dict(k=cache(7400 + 4 * i, kvh, cap, hd, np.float16),
+                 v=cache(7401 + 4 * i, kvh, cap, hd, np.float16),
+                 q=normal(7402 + 4 * i, n * h * hd).reshape(n, h, hd),
+                 pos0=pos0, n=n)
+        seqs.append(s)
+        dev.append(dict(k=to_dev(s["k"], gpu), v=to_dev(s["v"], gpu),
+                        q=to_dev(s["q"], gpu),
+                        out=torch.full((n, h, hd), float("nan"), device=gpu),
+                        cap=cap, n=n, pos0=pos0))
+    print(f"{path}: lengths {[s['n'] for s in seqs]}", flush=True)
+    with Attention(h, kvh, hd, 4096) as a:
+        a.run_dev(KV_F16, dev, path=path)
+        torch.cuda.synchronize()
+    worst = 0.0
+    for s, d in zip(seqs, dev):
+        ref = orc.run(np.ascontiguousarray(s["q"], np.float32), s["k"], s["v"],
+                      n_head=h, n_kv=kvh, hd=hd, pos0=s["pos0"], kv=KV_F16,
+                      threads=threads(), block=64)
+        out = d["out"].cpu().numpy()
+        assert np.isfinite(out).all()
+        err = abs_err(out, ref)
+        worst = max(worst, err if path == "prefill" else
+                    err / max(1.0, float(np.abs(ref).max())))
+    bar = TOL_F16_ABS if path == "prefill" else TOL_FLOAT_ABS
+    print(f"{path}: worst err {worst:.2e} (bar {bar:.0e})")
+    assert worst <= bar
