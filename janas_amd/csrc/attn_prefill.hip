@@ -404,8 +404,7 @@ __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8
        32 (ks / 2) + 16 (ks % 2) + 8 (e / 4) + 4 (l / 32) + e % 4 */
     h8 pa[2 * kNPB];
     float ls = 0.0f;
-#pragma unroll
-    for (int ks = 0; ks < 2 * kNPB; ks++) {
+    auto weights = [&](int ks) {
 #pragma unroll
         for (int e = 0; e < 8; e++)
             pa[ks][e] = (_Float16)__builtin_amdgcn_exp2f(sacc[ks / 2][8 * (ks % 2) + e]);
@@ -418,12 +417,15 @@ __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8
             ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pws[e]),
                                         h2{(_Float16)1.0f, (_Float16)1.0f},
                                         ls, false);
-    }
-    lsum += ls;
+    };
 
     /* O^T += V^T . P^T (PIPE: operands one k-step ahead, except at head
        size 512, whose 8 column tiles of read-ahead would not fit) */
     if constexpr (!PIPE || D > 256) {
+#pragma unroll
+        for (int ks = 0; ks < 2 * kNPB; ks++)
+            weights(ks);
+        lsum += ls;
 #pragma unroll
         for (int ks = 0; ks < 2 * kNPB; ks++)
 #pragma unroll
@@ -431,25 +433,32 @@ __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8
                 o[c] = mfma(vop(ks, c), pa[ks], o[c]);
         return;
     }
+    /* PIPE: k-step ks + 1's operands and weights are made while k-step
+       ks's products run */
     h8 va[2][CT];
 #pragma unroll
     for (int c = 0; c < CT; c++)
         va[0][c] = vop(0, c);
+    weights(0);
 #pragma unroll
     for (int ks = 0; ks < 2 * kNPB; ks++) {
-        if (ks + 1 < 2 * kNPB)
+        if (ks + 1 < 2 * kNPB) {
 #pragma unroll
             for (int c = 0; c < CT; c++)
                 va[(ks + 1) & 1][c] = vop(ks + 1, c);
+            weights(ks + 1);
+        }
 #pragma unroll
         for (int c = 0; c < CT; c++)
             o[c] = mfma(va[ks & 1][c], pa[ks], o[c]);
     }
+    lsum += ls;
     __builtin_amdgcn_sched_group_barrier(0x100, 2 * CT, 1);
 #pragma unroll
     for (int ks = 0; ks < 2 * kNPB; ks++) {
-        if (ks + 1 < 2 * kNPB)
+        if (ks + 1 < 2 * kNPB) {
             __builtin_amdgcn_sched_group_barrier(0x100, 2 * CT, 1);
+        }
         __builtin_amdgcn_sched_group_barrier(0x008, CT, 1);
     }
 }
