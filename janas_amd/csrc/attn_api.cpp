@@ -124,7 +124,8 @@ int describe(const janas_attn *a, int kv, const janas_attn_seq &s, SeqDesc &d)
     } else if (d.end > s.cap) {
         return JANAS_ATTN_ERANGE;
     }
-    d.rtiles = (s.n * a->group + 15) / 16;
+    const uint32_t tr = split_tile_rows(a->hd);
+    d.rtiles = (s.n * a->group + tr - 1) / tr;
     if (s.out_q8k && ((uint64_t)a->n_head * a->hd) % JANAS_ATTN_QK)
         return JANAS_ATTN_EINVAL;
     return JANAS_ATTN_OK;

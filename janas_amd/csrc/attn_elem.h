@@ -192,6 +192,41 @@ __device__ __forceinline__ u4 unit_fix(u4 x, bool back)
     return back ? u4{x.z, x.w, x.x, x.y} : x;
 }
 
+/* ---- cross-lane reductions without LDS: v_permlane16_swap /
+   v_permlane32_swap exchange rows of 16 (lanes l ^ 16) and halves of the
+   wave (l ^ 32); the pair they return holds a value and its partner's, in
+   lane order, so both lanes of a pair see the same operands ---- */
+__device__ __forceinline__ float max_x16(float a)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_x32(float a)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_x16(float a)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_x32(float a)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+/* lane l ^ 1's value (DPP quad_perm [1, 0, 3, 2]) */
+__device__ __forceinline__ float from_x1(float a)
+{
+    return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(a), 0xB1, 0xf, 0xf, false));
+}
+
+/* log2(e), and the reference's weight cutoff e^-80 (attention.c:580) in
+   powers of two: 80 / ln 2 */
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kCut2 = -115.41560327111707f;
+
 __device__ __forceinline__ uint32_t row_lo(const SplitArgs &A, uint32_t pos)
 {
     return A.window && pos + 1 > A.window ? pos + 1 - A.window : 0;

@@ -16,6 +16,11 @@ namespace janas {
 /* positions a chunk: partials are kept per chunk at absolute offsets, as
    the reference's ATT_CHUNK (attention.c:25) */
 constexpr uint32_t kChunk = 256;
+/* query rows a split-path workgroup takes: 8 at head sizes up to 256
+   (attn_split.hip), 16 above (attn_wide.hip) */
+constexpr uint32_t kTileRows = 8;
+constexpr uint32_t kWideRows = 16;
+inline uint32_t split_tile_rows(uint32_t hd) { return hd > 256 ? kWideRows : kTileRows; }
 /* sequences one launch takes (by value in its arguments) */
 constexpr uint32_t kMaxSeqs = 16;
 /* merge workgroups a launch keeps at least when it takes 128 columns a
@@ -36,7 +41,8 @@ struct SeqDesc {
     const uint32_t *last;  /* [n] or null: token j sees up to pos0 + j */
     uint32_t cap, n, pos0, end; /* end: 1 + the last position any token sees */
     uint32_t c0, span;     /* chunks c0 .. c0 + span - 1 are read */
-    uint32_t rtiles;       /* query-row tiles of 16 (rows = n x group) */
+    uint32_t rtiles;       /* query-row tiles of split_tile_rows(hd) rows
+                              (rows = n x group) */
     uint32_t wg0;          /* first workgroup of the split launch */
     uint32_t mg0;          /* first workgroup of the merge launch */
     uint32_t nseg;         /* prefill: key segments a row block is split

@@ -10,42 +10,34 @@
  * token's result does not depend on the block it runs in, and maps it onto
  * the GPU:
  *
- *   split kernel   one workgroup (8 waves of 64) per (sequence, KV head,
- *                  chunk, tile of 16 query rows); a query row is a (token,
- *                  query head of the KV head's group), so every K/V row of
- *                  the chunk is read once for the whole GQA group. Wave w
- *                  loads positions 32 w .. 32 w + 31 of K at once, then of V
- *                  as soon as its K is in, with contiguous 16-byte loads,
- *                  stages them through its own LDS region
- *                  into MFMA operand order, and computes a one-shot softmax
- *                  over its 32 positions; the 8 waves' partials are combined
- *                  in LDS in a fixed order into the chunk's exact partial.
- *                  Workgroups are renumbered so each XCD takes a contiguous
- *                  range (neighbouring chunks share an L2).
+ *   split kernel   one workgroup (4 waves of 64, one a SIMD) per (sequence,
+ *                  KV head, chunk, tile of 8 query rows); a query row is a
+ *                  (token, query head of the KV head's group), so every K/V
+ *                  row of the chunk is read once for the whole GQA group.
+ *                  Wave w streams positions 64 w .. 64 w + 63 in groups of
+ *                  16 with two groups in flight, scores each K group as it
+ *                  lands, takes a one-shot softmax over its 64 positions and
+ *                  the value product of each V group as it lands; the 4
+ *                  waves' partials are combined in LDS in a fixed order into
+ *                  the chunk's exact partial. Workgroups are renumbered so
+ *                  each XCD takes a contiguous range (neighbouring chunks
+ *                  share an L2).
  *   merge kernel   one workgroup per (token, query head, 32 or 128 columns): the
  *                  ordered merge of the chunk partials (8 groups of chunks in
  *                  parallel, each in batches of 16, combined in a fixed
  *                  tree), the output gate sigmoid(g) * o (model_attn.c:
  *                  159-170) fused in.
  *
- * Scores and values run on the matrix cores (v_mfma_f32_16x16x32_f16) at
- * float accuracy: the query and the weights are split into a high and a low
- * f16 part (x = hi + lo, 22 significant bits), each scaled by a power of two
- * first so that neither part loses bits to f16's range; keys and values
- * enter as f16 planes whose sum is the cached number exactly (int8 and f16:
- * one plane; int16: 256 * (x >> 8) and x & 255; f32: hi + lo). Products are
- * exact in the MFMA and summed in f32; for an f32 cache the product of the
- * two low parts (below 2^-22 of a term) is left out.
- *
- *   S^T = K . Q^T   wave w scores its 32 positions as two 16-position
- *                   tiles (A = K rows from LDS, B = the query planes from
- *                   LDS); lane l holds row l % 16 at positions 4 (l / 16) + i
- *                   of each tile - already the A layout of the value product.
- *   O   = P . V     the weights stay in registers as A operands; V is read
- *                   back transposed with ds_read_b64_tr_b16 (16-bit types,
- *                   and int8 rows widened to f16 as they are staged) or
- *                   gathered (f32 planes); every wave sums all value
- *                   columns over its positions.
+ * Scores and values run on the matrix cores at float accuracy: the query
+ * and the weights are split into a high and a low f16 part (x = hi + lo, 22
+ * significant bits), each scaled by a power of two first so that neither
+ * part loses bits to f16's range; keys and values enter as f16 planes whose
+ * sum is the cached number exactly (int8 and f16: one plane; int16:
+ * 256 * (x >> 8) and x & 255; f32: hi + lo). The two query (weight) planes
+ * of a row are neighbouring MFMA rows, so one product takes both. Products
+ * are exact in the MFMA and summed in f32. Scores, the partials' largest
+ * scores and the merge work in powers of two (log2 e folded into the score
+ * scale), so each exponential is one v_exp_f32.
  */
 #include <math.h>
 #include <stdint.h>
@@ -57,199 +49,215 @@
 namespace janas {
 namespace {
 
-/* ---- the split kernel: one shot, every load in flight at once -------- */
+/* ---- the split kernel: four waves, each streaming its positions ------- */
 
 /*
- * A workgroup is 8 waves (2 a SIMD); wave w takes positions 32 w .. 32 w + 31
- * of the chunk. Every wave issues its loads in two bursts - the tile's
- * query and its 32 K rows at once, then its 32 V rows as soon as the K rows
- * are in - 16 contiguous bytes a lane (1 KB a wave instruction, the pattern
- * that streams HBM fastest), so the chunk's 128 KB of K (head_dim 256, f16)
- * are in flight from the first microsecond and the scores overlap the V
- * transfer. Asking for V earlier - with K, or right after the query
- * barrier - measured slower (17.8 and 16.4 us against 15.7 us on a 32k
- * decode): K then lands later and the scores no longer overlap anything.
- * K rows pass through a private LDS region to become the MFMA's A operand;
- * the same region then holds the V rows, read back transposed. A wave's
- * softmax is one shot over its 32 positions; the 8 waves' (max, sum,
- * values) are combined at the end. No load goes straight to LDS: with
- * those in flight the compiler makes every barrier and every use of a
- * register load wait for all of them. In a decode K and V are read once,
- * so their loads are nontemporal (15.7 against 16.6 us on the 32k decode);
- * the row tiles of a block of tokens read a chunk each, and plain loads
- * keep it in L2 for them (the NT instance is the decode one: a branch
- * between the two in one kernel cost the decode 6 %).
+ * A workgroup is 4 waves, one a SIMD; wave w takes positions 64 w .. 64 w +
+ * 63 of the chunk as 4 groups of 16. The memory pipe of a SIMD serves its
+ * loads in issue order and only so many at once (an instruction that asks
+ * for more waits until earlier data lands), so a wave keeps two groups (its
+ * K, then its V) in flight: when group s has landed it asks for group s + 2
+ * and then computes on s - K groups 0..3, then V groups 0..3, 1 KB a load
+ * instruction. The scores of a group are computed as soon as its K is in;
+ * the softmax is one shot over the wave's 64 positions once all four K
+ * groups are scored; the value product takes each V group as it lands. The
+ * query's two planes are staged in LDS once, before the big loads are
+ * issued, so no score waits for a load queued behind the chunk.
+ *
+ * Query rows come in tiles of 8 (row r = token j x group + head): MFMA row
+ * 2 i is tile row i's high plane, 2 i + 1 its low plane, so a lane's two
+ * neighbours hold one query row's two partial sums (added across lanes l
+ * and l ^ 1 for the scores, and inside a lane for the values: output rows
+ * 2 i and 2 i + 1 land in the same lane).
+ *
+ *   S^T = K . Q^T   v_mfma_f32_16x16x32_f16 over the head dimension: A = a
+ *                   group's 16 K rows (LDS), B = the query planes (LDS);
+ *                   lane l holds MFMA row l % 16 at positions 4 (l / 16) + i.
+ *   O   = P . V     v_mfma_f32_16x16x16_f16 over the group's 16 positions:
+ *                   the weights are already its A operand; V is read back
+ *                   transposed (ds_read_b64_tr_b16).
+ *
+ * Every wave's (largest score, sum of weights, weighted values) is combined
+ * in LDS in a fixed order into the chunk's partial. Scores are kept in
+ * powers of two (log2 e folded into the score scale; the partial's largest
+ * score too), so every exponential is one v_exp_f32.
+ *
+ * Element types: f16 and int16 rows are staged as they are (int16 is split
+ * into 256 (x >> 8) and x & 255 when read), int8 rows are widened to f16,
+ * f32 rows are split into two f16 planes; every LDS row is head size x 16
+ * bits, its 16-byte units swizzled (unit u of row r in slot u ^ swz(r)) so
+ * that both operand reads are free of bank conflicts.
  */
-constexpr int kWaves = 8;
-constexpr int kWavePos = kChunk / kWaves; /* 32 */
+constexpr int kSW = 4;              /* waves a workgroup */
+constexpr int kSWP = kChunk / kSW;  /* positions a wave */
+constexpr int kSG = 16;             /* positions a group */
+constexpr int kSNG = kSWP / kSG;    /* groups a wave */
 
-template <int T, int D> struct Shape {
+template <int T, int D> struct SS {
     static constexpr int EB = Elem<T>::bytes;
-    static constexpr int P = Elem<T>::planes;
+    static constexpr int MRB = D * EB;               /* bytes of a padded row in memory */
+    static constexpr int LG = kSG * MRB / 1024;      /* 1 KB loads a group */
+    static constexpr int LRB = 2 * D;                /* bytes of an LDS row */
+    static constexpr int NPL = T == kF32 ? 2 : 1;    /* LDS planes */
+    static constexpr int PLB = kSG * LRB;            /* bytes of a plane */
+    static constexpr int REG = PLB * NPL;            /* a wave's region */
+    static constexpr int KS = D / 32;                /* score k-steps */
+    static constexpr int NT = D / 16;                /* value column tiles */
+    static constexpr int DP = Elem<T>::planes;       /* data planes a product */
     static constexpr bool SCALED = T == kI8 || T == kI16;
-    static constexpr int RB = D * EB;               /* bytes of a (padded) row */
-    static constexpr int WBYTES = kWavePos * RB;    /* a wave's K (or V) rows */
-    static constexpr int UNITS = WBYTES / 1024;     /* 16-byte loads a lane */
-    static constexpr int KS = D / 32;               /* score k-steps */
-    static constexpr int NT = D / 16;               /* output column tiles */
-    static constexpr int QV = D / 128 > 0 ? D / 128 : 1; /* q float4 a lane */
-    static constexpr int QP = D + 16;               /* halves a q row in LDS */
-    /* a wave's region: its rows (int8 values widened to f16: twice the
-       bytes), later its sums ([NT][64] f4) */
-    static constexpr int RROWS = (T == kI8 ? 2 : 1) * UNITS * kBlk;
-    static constexpr int RSUM = NT * 64 * 16;
-    static constexpr int REGION = RROWS > RSUM ? RROWS : RSUM;
-    static constexpr int VRB = T == kI8 ? 2 * RB : RB; /* bytes of a V row in LDS */
+    static_assert(LG >= 1 && kSG * MRB % 1024 == 0, "whole kilobytes a group");
+    static_assert(REG >= 32 * D, "the region holds the wave's sums");
 };
 
-/* ONE: a launch of one sequence - its descriptor is read at fixed offsets
-   with the rest of the arguments, not after the launch's sequence count (a
-   round trip to the arguments earlier for the first loads, 0.4 us a
-   decode) */
-template <int T, int D, bool NT, bool ONE = false>
-__global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
+/* the LDS slot of unit u of a row r (the units of a row: D / 8) */
+template <int D> __device__ __forceinline__ uint32_t slot(uint32_t u, uint32_t r)
 {
-    using E = Elem<T>;
-    using S = Shape<T, D>;
-    constexpr int P = S::P;
-    static_assert(S::UNITS >= 1 && S::WBYTES % 1024 == 0, "whole kilobytes a wave");
-    static_assert(2 * S::UNITS + 2 * S::QV + 16 < 63, "the loads fit the wait counter");
-    __shared__ __attribute__((aligned(16))) char sW[kWaves * S::REGION];
-    __shared__ __attribute__((aligned(16))) _Float16 sQ[2][kRows][S::QP];
-    __shared__ float sMax[kWaves][kRows], sSum[kWaves][kRows];
-    __shared__ float sQs[kRows];
-    __shared__ uint32_t sLo[kRows], sHi[kRows];
+    if constexpr (D >= 128)
+        return u ^ (((r << 1) | ((r >> 3) & 1)) & 15);
+    else
+        return u ^ ((r >> 1) & 7);
+}
+
+/* ONE: a launch of one sequence - its descriptor is read at fixed offsets
+   with the rest of the arguments, not after the launch's sequence count. NT:
+   every chunk is read by one workgroup (decode): nontemporal loads; the row
+   tiles of a block of tokens read a chunk each, and plain loads keep it in
+   L2 for them. */
+template <int T, int D, bool NT, bool ONE = false>
+__global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
+{
+    using S = SS<T, D>;
+    constexpr int KS = S::KS, NT_ = S::NT, LG = S::LG, DP = S::DP;
+    __shared__ __attribute__((aligned(1024))) char sR[kSW * S::REG];
+    __shared__ __attribute__((aligned(16))) _Float16 sQ[16][D + 8];
+    __shared__ float sQs[8];
+    __shared__ __attribute__((aligned(16))) float sM[kSW][8];
+    __shared__ __attribute__((aligned(16))) float sL[kSW][8];
+    __shared__ float sPe[kSW];
+    __shared__ float sKs[kSW][kSWP], sVs[kSW][kSWP];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const uint32_t g16 = lane >> 4, l16 = lane & 15;
+    const uint32_t g = lane >> 4, l16 = lane & 15;
     const uint32_t id = xcd_remap(blockIdx.x, A.n_wg);
     uint32_t si = 0;
     if constexpr (!ONE)
         si = seq_index(A, &SeqDesc::wg0, id);
     const SeqDesc &sq = A.seq[si];
     const uint32_t G = A.group, hd = A.hd;
-    /* the cache and query addresses with the first batch of argument loads
-       (otherwise the compiler asks for them just before the big loads, one
-       round trip later) */
+    /* the cache and query addresses with the first batch of argument loads */
     asm volatile("" ::"s"(sq.k), "s"(sq.v), "s"(sq.q), "s"(A.n_head));
     const uint32_t local = id - sq.wg0;
     const uint32_t rt = local % sq.rtiles;
     const uint32_t c = sq.c0 + (local / sq.rtiles) % sq.span;
     const uint32_t kvh = local / sq.rtiles / sq.span;
-    const uint32_t R = sq.n * G, r0 = rt * kRows;
-    const uint32_t t0 = c * kChunk;
+    const uint32_t R = sq.n * G, r0 = rt * kTileRows;
+    const uint32_t t0 = c * kChunk, plast = sq.end - 1;
 
     /* the tile's tokens see [lo(first), last(final)]: nothing of this chunk
        means no partial is needed (the merge does not read it) */
-    const uint32_t rows_here = R - r0 < kRows ? R - r0 : kRows;
+    const uint32_t rows_here = R - r0 < kTileRows ? R - r0 : kTileRows;
     const uint32_t jf = r0 / G, jl = (r0 + rows_here - 1) / G;
     const uint32_t lo_all = row_lo(A, sq.pos0 + jf);
-    const uint32_t hi_all = sq.last ? sq.last[jl] : sq.pos0 + jl;
+    uint32_t hi_all = sq.last ? sq.last[jl] : sq.pos0 + jl;
+    hi_all = hi_all < plast ? hi_all : plast;
     if (t0 > hi_all || t0 + kChunk <= lo_all)
         return;
-    const uint32_t p0w = t0 + w * kWavePos;
-    /* does any row see a position of this wave? (uniform in the wave) */
-    const bool active = p0w <= hi_all && p0w + kWavePos > lo_all;
-    const uint32_t plast = sq.end - 1;
-    /* rows of the chunk in the cache: contiguous, a ring's too (cap is a
-       multiple of the chunk) */
+    const uint32_t rlast = plast - t0;
     const size_t crow = (size_t)kvh * sq.cap + (A.ring ? t0 % sq.cap : t0);
-
-    /* rows: visible range (read before the big loads, whose count a wait
-       for last[] would otherwise include) */
-    if (tid < kRows) {
-        uint32_t r = r0 + tid;
-        uint32_t lo = 1, hi = 0;
-        if (r < R) {
-            uint32_t j = r / G;
-            lo = row_lo(A, sq.pos0 + j);
-            hi = sq.last ? sq.last[j] : sq.pos0 + j;
-        }
-        sLo[tid] = lo;
-        sHi[tid] = hi;
-    }
-
-    /* ---- every load, unconditional: rows past the call read its last
-       row, columns past hd column 0 - valid memory whose numbers are masked
-       or multiplied by zero weights ---- */
-    /* q: wave w takes rows 2 w and 2 w + 1, lane l row 2 w + l / 32 */
-    const uint32_t qrow = 2 * w + (lane >> 5);
-    float4 qv[S::QV];
-    bool qok[S::QV];
-    {
-        const uint32_t r = r0 + qrow < R ? r0 + qrow : r0;
-        const uint32_t j = r / G, h = kvh * G + r % G;
-        const float *src = sq.q + ((size_t)j * A.n_head + h) * hd;
-#pragma unroll
-        for (int i = 0; i < S::QV; i++) {
-            const uint32_t col = 4 * ((lane & 31) + 32 * i);
-            qok[i] = r0 + qrow < R && col < hd && col < D;
-            qv[i] = *(const float4 *)(src + (col < hd ? col : 0));
-        }
-    }
-    /* K and V: byte 1024 i + 16 lane of the wave's 32 rows */
-    /* the chunk's rows start at one address per block; a lane's byte
-       offset from it stays below kChunk rows, 32 bits (the loads take the
-       base in scalar registers and the offset in one vector register) */
-    u4 kraw[S::UNITS], vraw[S::UNITS];
-    const uint32_t rbytes = hd * S::EB, rlast = plast - t0;
+    const uint32_t rbytes = hd * S::EB;
     const char *const kbase = (const char *)sq.k + crow * rbytes;
     const char *const vbase = (const char *)sq.v + crow * rbytes;
-    uint32_t off[S::UNITS];
-    bool back[S::UNITS]; /* int8 rows of 8 mod 16 bytes: unit_at() */
-#pragma unroll
-    for (int i = 0; i < S::UNITS; i++) {
-        const uint32_t byte = i * 1024 + lane * 16;
-        const uint32_t row = byte / S::RB, cb = byte % S::RB;
-        const uint32_t p = w * kWavePos + row; /* from t0 */
-        uint32_t at;
-        if constexpr (S::EB == 1) {
-            at = unit_at(cb, hd, back[i]);
-        } else {
-            at = cb < hd * S::EB ? cb : 0;
-            back[i] = false;
-        }
-        off[i] = __umul24(p < rlast ? p : rlast, rbytes) + at;
-    }
-    /* NT: every chunk is read by one row tile (decode), once: nontemporal;
-       one that several row tiles read (blocks of tokens) should stay in L2 */
-    if constexpr (NT) {
-#pragma unroll
-        for (int i = 0; i < S::UNITS; i++)
-            kraw[i] = __builtin_nontemporal_load((const u4 *)(kbase + off[i]));
-    } else {
-#pragma unroll
-        for (int i = 0; i < S::UNITS; i++)
-            kraw[i] = *(const u4 *)(kbase + off[i]);
-    }
-    /* the scales of the lane's positions 16 mt + 4 g16 + i */
-    float ks8[8], vs8[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        ks8[e] = 1.0f;
-        vs8[e] = 1.0f;
-    }
-    if constexpr (S::SCALED) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const uint32_t p = w * kWavePos + 16 * (e / 4) + 4 * g16 + e % 4;
-            const uint32_t at = p < rlast ? p : rlast;
-            ks8[e] = sq.ks[crow + at];
-            vs8[e] = sq.vs[crow + at];
-        }
+
+    /* the lane's MFMA row: tile row qr = l16 / 2, plane l16 & 1; its
+       visible positions [rlo, rhi] */
+    const uint32_t qr = l16 >> 1, rq = r0 + qr;
+    const bool qok = rq < R;
+    uint32_t rlo = 1, rhi = 0;
+    if (qok) {
+        const uint32_t j = rq / G;
+        rlo = row_lo(A, sq.pos0 + j);
+        rhi = sq.last ? sq.last[j] : sq.pos0 + j;
+        rhi = rhi < plast ? rhi : plast;
     }
 
-    /* ---- q: scaled by 2^e so that the row's largest |q| lies in
-       [2^13, 2^14), split into f16 planes, into LDS ---- */
-    {
+    /* ---- the query: wave w loads tile rows 2 w, 2 w + 1 (D / 4 lanes a
+       row, a float4 each; columns past hd read column 0) ---- */
+    constexpr int QL = D / 4;                  /* lanes a query row */
+    constexpr int QN = QL >= 64 ? 2 : 1;        /* loads a lane */
+    float4 qv[QN];
+    uint32_t qrow[QN], qcol[QN];
+    /* lanes past the wave's two rows (head size 64) take none */
+    const bool qlane = QN == 2 || lane / QL < 2;
+#pragma unroll
+    for (int h = 0; h < QN; h++) {
+        const uint32_t e = QN == 2 ? lane : lane % QL;
+        qrow[h] = qlane ? 2 * w + (QN == 2 ? h : lane / QL) : kTileRows;
+        qcol[h] = 4 * e;
+        const uint32_t r = r0 + qrow[h] < R ? r0 + qrow[h] : r0;
+        const uint32_t j = r / G, hh = kvh * G + r % G;
+        const float *src = sq.q + ((size_t)j * A.n_head + hh) * hd;
+        qv[h] = *(const float4 *)(src + (qcol[h] < hd ? qcol[h] : 0));
+    }
+    /* the value and key scales of the wave's 64 positions, a lane each */
+    float ksv = 1.0f, vsv = 1.0f;
+    if constexpr (S::SCALED) {
+        const uint32_t p = w * kSWP + lane;
+        const uint32_t at = p < rlast ? p : rlast;
+        ksv = sq.ks[crow + at];
+        vsv = sq.vs[crow + at];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    /* ---- K and V, 1 KB a load: load l of group s covers padded bytes
+       1024 l + 16 lane of the group's 16 rows ---- */
+    u4 kr[kSNG][LG], vr[kSNG][LG];
+    uint32_t off[LG];
+    bool back[LG];
+#pragma unroll
+    for (int l = 0; l < LG; l++) {
+        const uint32_t b = 1024 * l + 16 * lane;
+        const uint32_t row = b / S::MRB, cb = b % S::MRB;
+        uint32_t at;
+        if constexpr (S::EB == 1) {
+            at = unit_at(cb, hd, back[l]);
+        } else {
+            at = cb < rbytes ? cb : 0;
+            back[l] = false;
+        }
+        off[l] = row * 0x10000u + at; /* row in the high half */
+    }
+    auto addr = [&](int s, int l) -> uint32_t {
+        const uint32_t p = w * kSWP + kSG * s + (off[l] >> 16);
+        return __umul24(p < rlast ? p : rlast, rbytes) + (off[l] & 0xFFFF);
+    };
+    auto kload = [&](int s) {
+#pragma unroll
+        for (int l = 0; l < LG; l++)
+            kr[s][l] = NT ? __builtin_nontemporal_load((const u4 *)(kbase + addr(s, l)))
+                          : *(const u4 *)(kbase + addr(s, l));
+    };
+    auto vload = [&](int s) {
+#pragma unroll
+        for (int l = 0; l < LG; l++)
+            vr[s][l] = NT ? __builtin_nontemporal_load((const u4 *)(vbase + addr(s, l)))
+                          : *(const u4 *)(vbase + addr(s, l));
+    };
+    kload(0);
+    __builtin_amdgcn_sched_barrier(0);
+    kload(1);
+    __builtin_amdgcn_sched_barrier(0);
+
+    /* ---- the query planes: scaled by 2^e so that the row's largest |q|
+       lies in [2^13, 2^14), split into f16 hi + lo, into LDS ---- */
+#pragma unroll
+    for (int h = 0; h < QN; h++) {
+        const bool ok = r0 + qrow[h] < R && qrow[h] < kTileRows;
+        const float x[4] = {qv[h].x, qv[h].y, qv[h].z, qv[h].w};
         float mx = 0.0f;
+        if (ok && qcol[h] < hd)
+            mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
 #pragma unroll
-        for (int i = 0; i < S::QV; i++)
-            if (qok[i])
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qv[i].x), fabsf(qv[i].y)),
-                                     fmaxf(fabsf(qv[i].z), fabsf(qv[i].w))));
-#pragma unroll
-        for (int o2 = 1; o2 < 32; o2 <<= 1)
+        for (int o2 = 1; o2 < QL; o2 <<= 1)
             mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
         int ex = 0;
         if (mx > 0.0f && mx < INFINITY) {
@@ -257,247 +265,268 @@ __global__ __launch_bounds__(512) void split_kernel(const SplitArgs A)
             ex = 14 - ex;
         }
         const float up = ldexpf(1.0f, ex);
-#pragma unroll
-        for (int i = 0; i < S::QV; i++) {
-            const uint32_t col = 4 * ((lane & 31) + 32 * i);
-            if (col >= D)
-                continue;
-            const float x[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
+        if (qrow[h] < kTileRows) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 _Float16 hi, lo;
-                split_hl(qok[i] ? x[e] * up : 0.0f, hi, lo);
-                sQ[0][qrow][col + e] = hi;
-                sQ[1][qrow][col + e] = lo;
+                split_hl(ok && qcol[h] < hd ? x[e] * up : 0.0f, hi, lo);
+                sQ[2 * qrow[h]][qcol[h] + e] = hi;
+                sQ[2 * qrow[h] + 1][qcol[h] + e] = lo;
             }
+            if (qcol[h] == 0)
+                sQs[qrow[h]] = ldexpf(1.0f, -ex);
         }
-        if ((lane & 31) == 0)
-            sQs[qrow] = ldexpf(1.0f, -ex);
     }
+    if constexpr (S::SCALED) {
+        sKs[w][lane] = ksv;
+        sVs[w][lane] = vsv;
+    }
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
+    h8 qb[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++)
+        qb[ks] = *(const h8 *)&sQ[l16][32 * ks + 8 * g];
+    const float qs2 = sQs[qr] * A.scale * kLog2e;
 
-    /* ---- K into the wave's region, then the scores of its two tiles of
-       16 positions (A = K rows 16 mt + l16, B = the query planes) ---- */
-    char *const reg = sW + (size_t)w * S::REGION;
+    char *const myR = sR + w * S::REG;
+    /* the group's 16 B of row `row`, byte cb of the padded row, into the
+       region (16-bit units; int8 widened, f32 split into two planes) */
+    auto stage = [&](const u4 &x0, int l) {
+        const uint32_t row = off[l] >> 16;
+        const uint32_t cb = (1024 * l + 16 * lane) % S::MRB;
+        char *rb = myR + row * S::LRB;
+        if constexpr (T == kF16 || T == kI16) {
+            *(u4 *)(rb + 16 * slot<D>(cb / 16, row)) = x0;
+        } else if constexpr (T == kI8) {
+            const u4 x = unit_fix(x0, back[l]);
+            *(h8 *)(rb + 16 * slot<D>(cb / 8, row)) = Elem<kI8>::widen(x.x, x.y);
+            *(h8 *)(rb + 16 * slot<D>(cb / 8 + 1, row)) = Elem<kI8>::widen(x.z, x.w);
+        } else {
+            h4 hi, lo;
 #pragma unroll
-    for (int i = 0; i < S::UNITS; i++)
-        *(u4 *)(reg + blk_off(i * 1024 + lane * 16)) =
-            S::EB == 1 ? unit_fix(kraw[i], back[i]) : kraw[i];
-    /* V once the wave's K is in */
-    if constexpr (NT) {
-#pragma unroll
-        for (int i = 0; i < S::UNITS; i++)
-            vraw[i] = __builtin_nontemporal_load((const u4 *)(vbase + off[i]));
-    } else {
-#pragma unroll
-        for (int i = 0; i < S::UNITS; i++)
-            vraw[i] = *(const u4 *)(vbase + off[i]);
-    }
-    f4 sacc[2];
-    {
-        f4 sa[2][2] = {{f4{0, 0, 0, 0}, f4{0, 0, 0, 0}}, {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}}};
-#pragma unroll
-        for (int k = 0; k < S::KS; k++) {
-            const h8 qb0 = *(const h8 *)&sQ[0][l16][32 * k + 8 * g16];
-            const h8 qb1 = *(const h8 *)&sQ[1][l16][32 * k + 8 * g16];
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                const uint32_t bo = (16 * mt + l16) * S::RB + (32 * k + 8 * g16) * S::EB;
-                typename E::Raw kr;
-                if constexpr (S::EB == 1) {
-                    kr.a = *(const uint2 *)(reg + blk_off(bo));
-                } else if constexpr (S::EB == 2) {
-                    kr.a = *(const uint4 *)(reg + blk_off(bo));
-                } else {
-                    kr.a = *(const uint4 *)(reg + blk_off(bo));
-                    kr.b = *(const uint4 *)(reg + blk_off(bo + 16));
-                }
-                h8 ka[P];
-                E::planes8(kr, ka);
-#pragma unroll
-                for (int kp = 0; kp < P; kp++) {
-                    if (use_pair<T>(kp, 0))
-                        sa[mt][0] = mfma(ka[kp], qb0, sa[mt][0]);
-                    if (use_pair<T>(kp, 1))
-                        sa[mt][1] = mfma(ka[kp], qb1, sa[mt][1]);
-                }
+            for (int e = 0; e < 4; e++) {
+                _Float16 a, b;
+                split_hl(__uint_as_float(x0[e]), a, b);
+                hi[e] = a;
+                lo[e] = b;
             }
+            const uint32_t u = cb / 32, half = (cb / 16) & 1;
+            *(h4 *)(rb + 16 * slot<D>(u, row) + 8 * half) = hi;
+            *(h4 *)(rb + S::PLB + 16 * slot<D>(u, row) + 8 * half) = lo;
         }
-        sacc[0] = sa[0][0] + sa[0][1];
-        sacc[1] = sa[1][0] + sa[1][1];
-    }
+    };
 
-    /* ---- the wave's softmax, one shot over its 32 positions: lane l holds
-       row l16 at positions 16 mt + 4 g16 + i ---- */
-    const uint32_t rlo = sLo[l16], rhi = sHi[l16];
-    const float qs = sQs[l16] * A.scale;
-    float sv[8];
+    /* ---- scores, a group at a time as its K lands (lane: MFMA row l16 at
+       positions 16 s + 4 g + i) ---- */
+    const uint32_t p0w = t0 + w * kSWP;
+    float sv[kSNG][4];
     float m = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const uint32_t p = p0w + 16 * (e / 4) + 4 * g16 + e % 4;
-        float x = -INFINITY;
-        if (active && p >= rlo && p <= rhi && p <= plast) {
-            x = sacc[e / 4][e % 4] * qs;
-            if constexpr (S::SCALED)
-                x *= ks8[e];
+    for (int s = 0; s < kSNG; s++) {
+        {
+            u4 t[LG];
+#pragma unroll
+            for (int l = 0; l < LG; l++)
+                t[l] = kr[s][l];
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 2 < kSNG)
+                kload(s + 2);
+            else
+                vload(s + 2 - kSNG);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s > 0)
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int l = 0; l < LG; l++)
+                stage(t[l], l);
         }
-        sv[e] = x;
-        m = fmaxf(m, x);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        f4 sa = f4{0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            h8 ka[DP];
+            const uint32_t sl = 16 * slot<D>(4 * ks + g, l16);
+            if constexpr (T == kI16) {
+                const uint4 raw = *(const uint4 *)(myR + l16 * S::LRB + sl);
+                Elem<kI16>::split(raw, ka[0], ka[1]);
+            } else {
+                ka[0] = *(const h8 *)(myR + l16 * S::LRB + sl);
+                if constexpr (T == kF32)
+                    ka[1] = *(const h8 *)(myR + S::PLB + l16 * S::LRB + sl);
+            }
+#pragma unroll
+            for (int dp = 0; dp < DP; dp++)
+                sa = mfma(ka[dp], qb[ks], sa);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t pl = kSG * s + 4 * g + i, p = p0w + pl;
+            float x = (sa[i] + from_x1(sa[i])) * qs2;
+            if constexpr (S::SCALED)
+                x *= sKs[w][pl];
+            sv[s][i] = p >= rlo && p <= rhi ? x : -INFINITY;
+            m = fmaxf(m, sv[s][i]);
+        }
     }
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
-    /* the weights' power of two: the largest (e^0 times the largest value
-       scale of the wave's positions) lands in [2^12, 2^13) */
+    m = max_x32(max_x16(m));
+
+    /* ---- the wave's softmax (powers of two); the weights' power of two
+       puts their largest (times the largest value scale) in [2^12, 2^13) */
     int pe = 13;
     if constexpr (S::SCALED) {
         float vm = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; e++)
-            vm = fmaxf(vm, vs8[e]);
-        vm = fmaxf(vm, __shfl_xor(vm, 16, 64));
-        vm = fmaxf(vm, __shfl_xor(vm, 32, 64));
+        for (int s = 0; s < kSNG; s++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                vm = fmaxf(vm, sVs[w][kSG * s + 4 * g + i]);
+        vm = max_x32(max_x16(vm));
         int ev = 0;
         if (vm > 0.0f && vm < INFINITY)
             frexpf(vm, &ev);
         pe = 13 - ev;
     }
     const float up = ldexpf(1.0f, pe);
+    const float mm = m == -INFINITY ? 0.0f : m;
     float lsum = 0.0f;
-    /* A operand of the value product: k-slot j is position 4 g16 + j (j < 4)
-       or 16 + 4 g16 + j - 4 - the scores' own layout */
-    h8 pa[2];
+    h4 pa[kSNG];
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const float x = sv[e];
-        float pw = 0.0f;
-        if (x != -INFINITY && x - m >= -80.0f)
-            pw = expf(x - m);
-        lsum += pw;
-        _Float16 hi, lo;
-        split_hl(pw * vs8[e] * up, hi, lo);
-        pa[0][e] = hi;
-        pa[1][e] = lo;
-    }
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
-
-    /* ---- V into the same region (the wave's reads of K are done: LDS
-       serves a wave in order), then the values ---- */
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if constexpr (T == kI8) {
-        /* int8 values widened to f16 rows (exact), read back transposed
-           like the 16-bit types */
+    for (int s = 0; s < kSNG; s++)
 #pragma unroll
-        for (int i = 0; i < S::UNITS; i++) {
-            const uint32_t byte = i * 1024 + lane * 16;
-            const uint32_t row = byte / S::RB, cb = byte % S::RB;
-            const u4 x = unit_fix(vraw[i], back[i]);
-            *(h8 *)(reg + blk_off(row * S::VRB + cb * 2)) = Elem<kI8>::widen(x.x, x.y);
-            *(h8 *)(reg + blk_off(row * S::VRB + cb * 2 + 16)) = Elem<kI8>::widen(x.z, x.w);
+        for (int i = 0; i < 4; i++) {
+            const float d = sv[s][i] - mm;
+            const float pw = d >= kCut2 ? __builtin_amdgcn_exp2f(d) : 0.0f;
+            lsum += pw;
+            float pv = pw * up;
+            if constexpr (S::SCALED)
+                pv *= sVs[w][kSG * s + 4 * g + i];
+            _Float16 hi, lo;
+            split_hl(pv, hi, lo);
+            pa[s][i] = (l16 & 1) ? lo : hi;
         }
-    } else {
-#pragma unroll
-        for (int i = 0; i < S::UNITS; i++)
-            *(u4 *)(reg + blk_off(i * 1024 + lane * 16)) =
-                S::EB == 1 ? unit_fix(vraw[i], back[i]) : vraw[i];
+    lsum = sum_x32(sum_x16(lsum));
+    if (lane < 16 && !(lane & 1)) {
+        sM[w][lane >> 1] = m;
+        sL[w][lane >> 1] = lsum;
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    f4 o[S::NT];
+    if (lane == 0)
+        sPe[w] = ldexpf(1.0f, -pe);
+
+    /* ---- values, a group at a time as its V lands ---- */
+    f4 o[NT_];
 #pragma unroll
-    for (int t = 0; t < S::NT; t++)
+    for (int t = 0; t < NT_; t++)
         o[t] = f4{0, 0, 0, 0};
-    {
-        h8 vbp[S::NT][P];
+    const uint32_t r1 = 4 * g + (l16 >> 2);
 #pragma unroll
-        for (int t = 0; t < S::NT; t++) {
-            if constexpr (S::EB == 2 || T == kI8) {
-                const uint32_t r1 = 4 * g16 + (l16 >> 2);
-                const uint32_t cc = 16 * t + 4 * (l16 & 3);
-                const h4 x = lds_read_tr((const _Float16 *)(reg + blk_off(r1 * S::VRB + cc * 2)));
-                const h4 y = lds_read_tr((const _Float16 *)(reg + blk_off((r1 + 16) * S::VRB + cc * 2)));
-                const h8 xy = h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-                if constexpr (T == kF16 || T == kI8)
-                    vbp[t][0] = xy;
-                else
-                    Elem<kI16>::split(__builtin_bit_cast(uint4, xy), vbp[t][0], vbp[t][1]);
-            } else {
-                /* f32: the 8 positions of one column, one by one */
-                const uint32_t cc = 16 * t + l16;
+    for (int s = 0; s < kSNG; s++) {
+        {
+            u4 t[LG];
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const uint32_t rv = 16 * (e / 4) + 4 * g16 + e % 4;
-                    const uint32_t bo = blk_off(rv * S::RB + cc * S::EB);
-                    _Float16 hi, lo;
-                    split_hl(*(const float *)(reg + bo), hi, lo);
-                    vbp[t][0][e] = hi;
-                    vbp[t][1][e] = lo;
+            for (int l = 0; l < LG; l++)
+                t[l] = vr[s][l];
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 2 < kSNG)
+                vload(s + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int l = 0; l < LG; l++)
+                stage(t[l], l);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        h4 vb[NT_][DP];
+#pragma unroll
+        for (int t = 0; t < NT_; t++) {
+            const uint32_t cc = 16 * t + 4 * (l16 & 3);
+            const uint32_t a = r1 * S::LRB + 16 * slot<D>(cc / 8, r1) + (cc % 8) * 2;
+            if constexpr (T == kI16) {
+                const h4 x = lds_read_tr((const _Float16 *)(myR + a));
+                const uint2 u = __builtin_bit_cast(uint2, x);
+                const uint32_t wv[2] = {u.x, u.y};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int xi = (int)(int16_t)(wv[e / 2] >> (16 * (e % 2)));
+                    vb[t][0][e] = (_Float16)(float)((xi >> 8) * 256);
+                    vb[t][1][e] = (_Float16)(xi & 255);
                 }
+            } else {
+                vb[t][0] = lds_read_tr((const _Float16 *)(myR + a));
+                if constexpr (T == kF32)
+                    vb[t][1] = lds_read_tr((const _Float16 *)(myR + S::PLB + a));
             }
         }
-        /* columns past hd hold column 0's numbers: their sums are dropped */
 #pragma unroll
-        for (int ap = 0; ap < 2; ap++)
+        for (int t = 0; t < NT_; t++)
 #pragma unroll
-            for (int pp = 0; pp < P; pp++)
-                if (use_pair<T>(pp, ap))
-#pragma unroll
-                    for (int t = 0; t < S::NT; t++)
-                        o[t] = mfma(pa[ap], vbp[t][pp], o[t]);
+            for (int dp = 0; dp < DP; dp++)
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[s], vb[t][dp], o[t], 0, 0, 0);
     }
 
-    /* ---- the 8 waves combined: chunk max M, wave w's sums weighted by
-       e^(m_w - M) (and back to 2^0), then wave w adds up its column tiles
-       over the waves in a fixed order and writes them ---- */
-    if (lane < 16) {
-        sMax[w][lane] = m;
-        sSum[w][lane] = lsum;
-    }
-    __syncthreads();
-    float mc = -INFINITY;
+    /* ---- the waves combined: tile row 2 g + h's sums are o[t][2 h] +
+       o[t][2 h + 1] (high and low weights); into the region, then wave w
+       sums its tiles over the waves with weights 2^(m_w - M) 2^-pe_w ---- */
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    float2 *mine = (float2 *)myR;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ww++)
-        mc = fmaxf(mc, sMax[ww][l16]);
-    {
-        const float f = (m == -INFINITY ? 0.0f : expf(m - mc)) * ldexpf(1.0f, -pe);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float fi = __shfl(f, 4 * g16 + i, 64);
-#pragma unroll
-            for (int t = 0; t < S::NT; t++)
-                o[t][i] *= fi;
-        }
-    }
-    /* the region's V reads are done (in order); sums as [NT][64] f4 */
-    f4 *mine = (f4 *)reg;
-#pragma unroll
-    for (int t = 0; t < S::NT; t++)
-        mine[t * 64 + lane] = o[t];
+    for (int t = 0; t < NT_; t++)
+        mine[t * 64 + lane] = make_float2(o[t][0] + o[t][1], o[t][2] + o[t][3]);
     __syncthreads();
     const uint64_t prow = sq.part0 + ((uint64_t)kvh * sq.span + (c - sq.c0)) * R + r0;
-    for (uint32_t t = w; t < (uint32_t)S::NT; t += kWaves) {
-        f4 part[kWaves];
+    {
+        /* lane jj of a tile: source lanes 2 jj, 2 jj + 1 - tile rows 2 gs,
+           2 gs + 1 of columns cs, cs + 1 */
+        const uint32_t jj = lane & 31, gs = jj >> 3;
+        float fw[kSW][2];
 #pragma unroll
-        for (int ww = 0; ww < kWaves; ww++)
-            part[ww] = ((const f4 *)(sW + (size_t)ww * S::REGION))[t * 64 + lane];
-        const f4 sum = ((part[0] + part[1]) + (part[2] + part[3])) +
-                       ((part[4] + part[5]) + (part[6] + part[7]));
+        for (int h = 0; h < 2; h++) {
+            float mc = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t row = 4 * g16 + i, col = 16 * t + l16;
-            if (r0 + row < R && col < hd)
-                A.part_acc[(prow + row) * hd + col] = sum[i];
+            for (int ww = 0; ww < kSW; ww++)
+                mc = fmaxf(mc, sM[ww][2 * gs + h]);
+#pragma unroll
+            for (int ww = 0; ww < kSW; ww++) {
+                const float mw = sM[ww][2 * gs + h];
+                fw[ww][h] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mc) * sPe[ww];
+            }
+        }
+        constexpr int TPW = NT_ / kSW;   /* tiles a wave: 1, 2 or 4 */
+#pragma unroll
+        for (int tt = 0; tt < (TPW + 1) / 2; tt++) {
+            const uint32_t t = TPW * w + 2 * tt + (lane >> 5);
+            if (TPW == 1 && lane >= 32)
+                break;
+            const uint32_t cs = 16 * t + ((2 * jj) & 15);
+            f4 part[kSW];
+#pragma unroll
+            for (int ww = 0; ww < kSW; ww++)
+                part[ww] = ((const f4 *)(sR + ww * S::REG))[t * 32 + jj];
+            float res[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                res[i] = (part[0][i] * fw[0][i % 2] + part[1][i] * fw[1][i % 2]) +
+                         (part[2][i] * fw[2][i % 2] + part[3][i] * fw[3][i % 2]);
+            if (cs < hd) {
+                if (r0 + 2 * gs < R)
+                    *(float2 *)&A.part_acc[(prow + 2 * gs) * hd + cs] = make_float2(res[0], res[2]);
+                if (r0 + 2 * gs + 1 < R)
+                    *(float2 *)&A.part_acc[(prow + 2 * gs + 1) * hd + cs] = make_float2(res[1], res[3]);
+            }
         }
     }
-    if (w == 0 && lane < kRows && r0 + lane < R) {
-        float l = 0.0f;
+    if (w == 0 && lane < kTileRows && r0 + lane < R) {
+        float mc = -INFINITY;
 #pragma unroll
-        for (int ww = 0; ww < kWaves; ww++) {
-            const float mw = sMax[ww][lane];
-            l += (mw == -INFINITY ? 0.0f : expf(mw - mc)) * sSum[ww][lane];
+        for (int ww = 0; ww < kSW; ww++)
+            mc = fmaxf(mc, sM[ww][lane]);
+        float l[kSW];
+#pragma unroll
+        for (int ww = 0; ww < kSW; ww++) {
+            const float mw = sM[ww][lane];
+            l[ww] = (mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mc)) * sL[ww][lane];
         }
-        A.part_ml[(prow + lane) * 2] = mc;
-        A.part_ml[(prow + lane) * 2 + 1] = l;
+        *(float2 *)&A.part_ml[(prow + lane) * 2] = make_float2(mc, (l[0] + l[1]) + (l[2] + l[3]));
     }
 }
 
@@ -545,7 +574,10 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     const uint32_t h = (local / nd) % A.n_head, j = local / nd / A.n_head;
     const uint32_t kvh = h / G, r = j * G + h % G, R = sq.n * G;
     const uint32_t pos = sq.pos0 + j;
-    const uint32_t lo = row_lo(A, pos), hi = sq.last ? sq.last[j] : pos;
+    /* last[] past the call's end would read partials of other rows */
+    uint32_t hi = sq.last ? sq.last[j] : pos;
+    hi = hi < sq.end - 1 ? hi : sq.end - 1;
+    const uint32_t lo = row_lo(A, pos);
     const uint32_t clo = lo / kChunk, nc = hi / kChunk - clo + 1;
     /* partial row of chunk clo + i */
     const uint64_t base = sq.part0 + ((uint64_t)kvh * sq.span + (clo - sq.c0)) * R + r;
@@ -589,15 +621,16 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
         for (int b = 0; b < kMergeBatch; b++)
             if (i0 + kMergeGroups * b < nc)
                 mb = fmaxf(mb, ml[b].x);
-        /* the batch's sums, against the group's new largest score */
-        const float f = mg == -INFINITY ? 0.0f : expf(mg - mb);
+        /* the batch's sums, against the group's new largest score (scores
+           in powers of two) */
+        const float f = mg == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mg - mb);
         lg *= f;
 #pragma unroll
         for (int e = 0; e < CPL; e++)
             f4e(ag, e) *= f;
 #pragma unroll
         for (int b = 0; b < kMergeBatch; b++) {
-            const float wgt = i0 + kMergeGroups * b < nc ? expf(ml[b].x - mb) : 0.0f;
+            const float wgt = i0 + kMergeGroups * b < nc ? __builtin_amdgcn_exp2f(ml[b].x - mb) : 0.0f;
             lg += wgt * ml[b].y;
 #pragma unroll
             for (int e = 0; e < CPL; e++)
@@ -621,7 +654,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     float4 wa[kMergeGroups];
 #pragma unroll
     for (int k = 0; k < kMergeGroups; k++) {
-        const float wk = sM[k] == -INFINITY ? 0.0f : expf(sM[k] - mx);
+        const float wk = sM[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sM[k] - mx);
         float4 a = sAcc[k][cl];
         wl[k] = wk * sL[k];
 #pragma unroll
@@ -654,11 +687,11 @@ template <int T, int D>
 hipError_t launch_t(const SplitArgs &a, hipStream_t s)
 {
     if (a.once && a.n_seqs == 1)
-        hipLaunchKernelGGL((split_kernel<T, D, true, true>), dim3(a.n_wg), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((split_kernel<T, D, true, true>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
     else if (a.once)
-        hipLaunchKernelGGL((split_kernel<T, D, true>), dim3(a.n_wg), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((split_kernel<T, D, true>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
     else
-        hipLaunchKernelGGL((split_kernel<T, D, false>), dim3(a.n_wg), dim3(512), 0, s, a);
+        hipLaunchKernelGGL((split_kernel<T, D, false>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
     return hipGetLastError();
 }
 
@@ -682,8 +715,9 @@ hipError_t launch_d(uint32_t hd, const SplitArgs &a, hipStream_t s)
 int split_supported(int kv, uint32_t hd)
 {
     /* f32 rows above 128 numbers would not leave two stages in LDS; 8- and
-       16-bit rows above 256 take the wide kernel (attn_wide.hip) */
-    return kv >= kI8 && kv <= kF32 && hd >= 8 && hd % 8 == 0 &&
+       16-bit rows above 256 take the wide kernel (attn_wide.hip). An int8
+       row is read 16 bytes at a time, so it needs 16 bytes at least. */
+    return kv >= kI8 && kv <= kF32 && hd >= (kv == kI8 ? 16u : 8u) && hd % 8 == 0 &&
            hd <= (kv == kF32 ? 128u : 512u);
 }
 

@@ -155,6 +155,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
             uint32_t j = r / G;
             lo = row_lo(A, sq.pos0 + j);
             hi = sq.last ? sq.last[j] : sq.pos0 + j;
+            hi = hi < sq.end - 1 ? hi : sq.end - 1;
         }
         sLo[tid] = lo;
         sHi[tid] = hi;
@@ -248,7 +249,8 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     __syncthreads();
 
     const uint32_t rlo = sLo[l16], rhi = sHi[l16];
-    const float qs = sQs[l16] * A.scale;
+    /* scores in powers of two: log2 e folded into the scale */
+    const float qs = sQs[l16] * A.scale * kLog2e;
     /* this lane's positions of round r: 16 r + 4 g16 + i of the wave */
     const uint32_t pl = w * kWPos + 4 * g16;
     char *const reg = sW + (size_t)w * S::REGION;
@@ -387,8 +389,8 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
             for (int e = 0; e < 4 * kRounds; e++) {
                 const float x = sv[e];
                 float pw = 0.0f;
-                if (x != -INFINITY && x - m >= -80.0f)
-                    pw = expf(x - m);
+                if (x != -INFINITY && x - m >= kCut2)
+                    pw = __builtin_amdgcn_exp2f(x - m);
                 lsum += pw;
                 _Float16 hi, lo;
                 split_hl(pw * vsc[e] * up, hi, lo);
@@ -410,7 +412,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     step(std::integral_constant<int, 7>());
 
     /* ---- the 4 waves combined: chunk max M, wave w's sums weighted by
-       e^(m_w - M) (and back to 2^0), then summed over the waves in a fixed
+       2^(m_w - M) (and back to 2^0), then summed over the waves in a fixed
        order, half the column tiles at a time ---- */
     if (lane < 16) {
         sMax[w][lane] = m;
@@ -422,7 +424,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     for (int ww = 0; ww < kWWaves; ww++)
         mc = fmaxf(mc, sMax[ww][l16]);
     {
-        const float f = (m == -INFINITY ? 0.0f : expf(m - mc)) * ldexpf(1.0f, -pe);
+        const float f = (m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mc)) * ldexpf(1.0f, -pe);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const float fi = __shfl(f, 4 * g16 + i, 64);
@@ -464,7 +466,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 #pragma unroll
         for (int ww = 0; ww < kWWaves; ww++) {
             const float mw = sMax[ww][lane];
-            l += (mw == -INFINITY ? 0.0f : expf(mw - mc)) * sSum[ww][lane];
+            l += (mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mc)) * sSum[ww][lane];
         }
         A.part_ml[(prow + lane) * 2] = mc;
         A.part_ml[(prow + lane) * 2 + 1] = l;
