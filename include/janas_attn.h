@@ -19,10 +19,15 @@
  * Errors. janas_attn_create returns NULL on a geometry the reference
  * rejects (attention.c:998-1000) or when the device cannot be used.
  * janas_attn_run is void, as the reference's: a call the reference would
- * abort on (a ring too small, attention.c:1281-1286) aborts with a message,
- * and so does a device failure - there is no CPU path behind it to fall
- * back on. The Part 2 entry points return 0 or a negative JANAS_ATTN_E*
- * code and never abort.
+ * abort on (a ring too small, attention.c:1281-1286) aborts with a message.
+ * A device failure is remembered in the instance (janas_attn_status, sticky
+ * until cleared) - the reference's GPU backend likewise marks itself broken
+ * and the engine carries on on the CPU (gpu_cuda.c:614-616, model.c:698-
+ * 705). By default janas_attn_run then aborts, since the library has no CPU
+ * path; after janas_attn_set_abort(a, 0) it returns instead, with a host
+ * output filled with NaN, so the engine can check the status and fall back
+ * to its own attention. The Part 2 entry points return 0 or a negative
+ * JANAS_ATTN_E* code, never abort, and remember device failures too.
  */
 #ifndef JANAS_ATTN_HIP_H
 #define JANAS_ATTN_HIP_H
@@ -93,6 +98,16 @@ void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
                     const float *q, const int8_t *k, const float *ks,
                     const int8_t *v, const float *vs, uint32_t n,
                     uint32_t pos0, float *out);
+
+/* The instance's first device failure since create or the last clear (a
+   negative JANAS_ATTN_E* code; argument errors are not kept), or 0.
+   No counterpart in attention.h: the reference marks its GPU backend
+   broken (gpu_cuda.c:614-616) and the engine tests that flag. */
+int janas_attn_status(const struct janas_attn *a);
+void janas_attn_clear_status(struct janas_attn *a);
+/* 1 (the default): janas_attn_run aborts on a device failure; 0: it
+   returns, the output (host memory) filled with NaN. */
+void janas_attn_set_abort(struct janas_attn *a, int on);
 
 /* ===== Part 2: the device extension (no counterpart in the reference) = */
 

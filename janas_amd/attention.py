@@ -26,6 +26,7 @@ KV_I8, KV_I16, KV_F16, KV_F32 = 0, 1, 2, 3
 GATE_NONE, GATE_ELEM, GATE_HEAD = 0, 1, 2
 ERRORS = {0: "ok", -1: "EINVAL", -2: "ERANGE", -3: "ENOMEM", -4: "EDEVICE",
           -5: "ENOTSUP"}
+OK, EINVAL, ERANGE, ENOMEM, EDEVICE, ENOTSUP = 0, -1, -2, -3, -4, -5
 
 _u32 = ctypes.c_uint32
 _vp = ctypes.c_void_p
@@ -99,6 +100,12 @@ def lib():
                                              ctypes.POINTER(Seq), _u32, _vp,
                                              ctypes.c_int]
     L.janas_attn_run_dev_kernels.restype = ctypes.c_int
+    L.janas_attn_status.argtypes = [_vp]
+    L.janas_attn_status.restype = ctypes.c_int
+    L.janas_attn_clear_status.argtypes = [_vp]
+    L.janas_attn_clear_status.restype = None
+    L.janas_attn_set_abort.argtypes = [_vp, ctypes.c_int]
+    L.janas_attn_set_abort.restype = None
     L.janas_attn_strerror.argtypes = [ctypes.c_int]
     L.janas_attn_strerror.restype = ctypes.c_char_p
     L.janas_attn_cache_write.argtypes = [ctypes.POINTER(Cache), _vp, _vp,
@@ -214,6 +221,18 @@ class Attention:
         lib().janas_attn_run(self._a, None, ptr(q), ptr(k), ptr(ks), ptr(v),
                              ptr(vs), n, pos0, ptr(out))
         self._last = None
+
+    def status(self):
+        """janas_attn_status: the first device failure kept, or 0."""
+        return lib().janas_attn_status(self._a)
+
+    def clear_status(self):
+        lib().janas_attn_clear_status(self._a)
+
+    def set_abort(self, on):
+        """janas_attn_set_abort: whether janas_attn_run aborts on a
+        failure (the default) or returns with a NaN output."""
+        lib().janas_attn_set_abort(self._a, 1 if on else 0)
 
     def prepare(self, kv_type, seqs, gate_mode=GATE_NONE, stream=None,
                 path="auto"):

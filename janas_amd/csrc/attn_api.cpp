@@ -43,11 +43,22 @@ struct janas_attn {
     /* partials: part_rows rows of (m, l) and of hd values */
     float *part_ml, *part_acc;
     uint64_t part_rows;
-    /* staging of host pointers for janas_attn_run */
+    /* the stream that last used the partials: a call on another stream
+       waits for its work first (part_ev), and the partials are freed only
+       once it is done */
+    hipStream_t part_stream;
+    hipEvent_t part_ev;
+    /* staging of host pointers for janas_attn_run, and the bytes each
+       staging buffer holds */
     float *st_q, *st_out;
     void *st_k, *st_v;
     float *st_ks, *st_vs;
     uint32_t *st_last;
+    size_t st_k_bytes, st_v_bytes, st_ks_bytes, st_vs_bytes;
+    /* the first device failure since create (or the last clear): sticky;
+       abort_on_error: janas_attn_run aborts on one (the default) */
+    int status;
+    int abort_on_error;
     /* timing */
     int prof;
     std::vector<ProfEv> *ev_used, *ev_free;
@@ -153,13 +164,42 @@ int put_q8k(const janas_attn *a, const janas_attn_seq *seqs, uint32_t n_seqs,
     return JANAS_ATTN_OK;
 }
 
+/* A device failure is remembered (janas_attn_status) as well as returned. */
+int note(janas_attn *a, int rc)
+{
+    if (rc && !a->status && rc != JANAS_ATTN_EINVAL && rc != JANAS_ATTN_ERANGE &&
+        rc != JANAS_ATTN_ENOTSUP)
+        a->status = rc;
+    return rc;
+}
+
+/* The partials are about to be used on `stream`: if another stream used
+   them last, this one first waits for everything queued there so far. */
+int part_sync(janas_attn *a, hipStream_t stream)
+{
+    if (a->part_stream != stream) {
+        if (a->part_stream) {
+            hipError_t e = hipEventRecord(a->part_ev, a->part_stream);
+            if (e == hipSuccess)
+                e = hipStreamWaitEvent(stream, a->part_ev, 0);
+            if (e != hipSuccess)
+                return hip_err(e, "order the partials' streams");
+        }
+        a->part_stream = stream;
+    }
+    return JANAS_ATTN_OK;
+}
+
 int ensure_part(janas_attn *a, uint64_t rows, hipStream_t stream)
 {
     if (rows <= a->part_rows)
         return JANAS_ATTN_OK;
-    /* the stream may still read the old ones */
+    /* the stream that used them last, and this one, may still read the
+       old ones */
     if (a->part_ml || a->part_acc) {
         hipError_t e = hipStreamSynchronize(stream);
+        if (e == hipSuccess && a->part_stream && a->part_stream != stream)
+            e = hipStreamSynchronize(a->part_stream);
         if (e != hipSuccess)
             return hip_err(e, "synchronize");
         (void)hipFree(a->part_ml);
@@ -177,6 +217,26 @@ int ensure_part(janas_attn *a, uint64_t rows, hipStream_t stream)
     }
     a->part_rows = rows;
     return JANAS_ATTN_OK;
+}
+
+/* Where a call's partials live: the instance's (grown as needed, ordered
+   across streams), or the device's fixed array of the allocation-free
+   entry point (a call that needs more rows is refused). */
+struct Parts {
+    float *ml, *acc;
+    bool fixed;
+};
+
+int get_parts(janas_attn *a, uint64_t rows, hipStream_t stream, bool fixed, Parts &p)
+{
+    (void)fixed;
+    int rc = ensure_part(a, rows, stream);
+    if (!rc)
+        rc = part_sync(a, stream);
+    p.ml = a->part_ml;
+    p.acc = a->part_acc;
+    p.fixed = false;
+    return rc;
 }
 
 ProfEv *prof_begin(janas_attn *a, int kind, hipStream_t stream)
@@ -204,10 +264,10 @@ void prof_end(ProfEv *ev, hipStream_t stream)
         (void)hipEventRecord(ev->b, stream);
 }
 
-int fill_args(const janas_attn *a, SplitArgs &args, int gate_mode)
+int fill_args(const janas_attn *a, SplitArgs &args, int gate_mode, const Parts &p)
 {
-    args.part_ml = a->part_ml;
-    args.part_acc = a->part_acc;
+    args.part_ml = p.ml;
+    args.part_acc = p.acc;
     args.n_head = a->n_head;
     args.n_kv = a->n_kv;
     args.group = a->group;
@@ -220,7 +280,7 @@ int fill_args(const janas_attn *a, SplitArgs &args, int gate_mode)
 }
 
 int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
-              uint32_t n_seqs, hipStream_t stream, int kernels = 3)
+              uint32_t n_seqs, hipStream_t stream, int kernels = 3, bool fixed = false)
 {
     if (!split_supported(kv, a->hd))
         return JANAS_ATTN_ENOTSUP;
@@ -252,21 +312,22 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
             mg += (uint32_t)nmg;
             rows += (uint64_t)a->n_kv * d.span * d.n * a->group;
         }
-        int rc = ensure_part(a, rows, stream);
+        Parts pt;
+        int rc = get_parts(a, rows, stream, fixed, pt);
         if (rc)
             return rc;
         args.n_seqs = m;
         args.n_wg = wg;
-        fill_args(a, args, gate_mode);
+        fill_args(a, args, gate_mode, pt);
         if (kernels & 1) {
-            ProfEv *ev = prof_begin(a, 0, stream);
+            ProfEv *ev = fixed ? nullptr : prof_begin(a, 0, stream);
             hipError_t e = launch_split(kv, args, stream);
             prof_end(ev, stream);
             if (e != hipSuccess)
                 return hip_err(e, "split launch");
         }
         if (kernels & 2) {
-            ProfEv *ev = prof_begin(a, 1, stream);
+            ProfEv *ev = fixed ? nullptr : prof_begin(a, 1, stream);
             hipError_t e = launch_merge(args, mg, stream);
             prof_end(ev, stream);
             if (e != hipSuccess)
@@ -299,7 +360,8 @@ uint32_t prefill_segments(const janas_attn *a, const SeqDesc &d)
 }
 
 int run_prefill(janas_attn *a, int kv, int gate_mode,
-                const janas_attn_seq *seqs, uint32_t n_seqs, hipStream_t stream)
+                const janas_attn_seq *seqs, uint32_t n_seqs, hipStream_t stream,
+                bool fixed = false)
 {
     if (!prefill_supported(kv, a->hd))
         return JANAS_ATTN_ENOTSUP;
@@ -332,13 +394,14 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
             wg += (uint32_t)nwg;
             mg += (uint32_t)nmg;
         }
+        Parts pt{nullptr, nullptr, fixed};
         if (rows) {
-            int rc = ensure_part(a, rows, stream);
+            int rc = get_parts(a, rows, stream, fixed, pt);
             if (rc)
                 return rc;
         }
-        args.part_ml = a->part_ml;
-        args.part_acc = a->part_acc;
+        args.part_ml = pt.ml;
+        args.part_acc = pt.acc;
         args.n_seqs = m;
         args.n_wg = wg;
         args.n_head = a->n_head;
@@ -349,7 +412,7 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
         args.scale = a->scale;
         args.ring = a->ring;
         args.gate_mode = gate_mode;
-        ProfEv *ev = prof_begin(a, 2, stream);
+        ProfEv *ev = fixed ? nullptr : prof_begin(a, 2, stream);
         hipError_t e = launch_prefill(kv, args, stream);
         if (e == hipSuccess && mg)
             e = launch_prefill_merge(args, mg, stream);
@@ -370,7 +433,7 @@ int check_call(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
         if (gate_mode != kGateNone && !seqs[i].gate)
             return JANAS_ATTN_EINVAL;
     hipError_t e = hipSetDevice(a->dev);
-    return e == hipSuccess ? JANAS_ATTN_OK : hip_err(e, "set device");
+    return e == hipSuccess ? JANAS_ATTN_OK : note(a, hip_err(e, "set device"));
 }
 
 [[noreturn]] void die(const char *what, int rc)
@@ -438,10 +501,14 @@ extern "C" struct janas_attn *janas_attn_create(uint32_t n_head,
     a->scores_auto = scores == JANAS_ATTN_AUTO;
     a->ev_used = new std::vector<ProfEv>();
     a->ev_free = new std::vector<ProfEv>();
-    if (hipStreamCreateWithFlags(&a->stream, hipStreamNonBlocking) !=
-        hipSuccess) {
+    a->abort_on_error = 1;
+    /* a blocking stream: the calls that run on it (janas_attn_run, and
+       Part 2 with a NULL stream) are ordered after work the caller queued
+       on the legacy default stream - row writes, copies - and before what
+       it queues there next */
+    if (hipStreamCreateWithFlags(&a->stream, hipStreamDefault) != hipSuccess ||
+        hipEventCreateWithFlags(&a->part_ev, hipEventDisableTiming) != hipSuccess) {
         (void)hipGetLastError();
-        a->stream = nullptr;
         janas_attn_destroy(a);
         return nullptr;
     }
@@ -464,6 +531,8 @@ extern "C" void janas_attn_destroy(struct janas_attn *a)
     (void)hipSetDevice(a->dev);
     if (a->stream)
         (void)hipStreamSynchronize(a->stream);
+    if (a->part_stream && a->part_stream != a->stream)
+        (void)hipStreamSynchronize(a->part_stream);
     (void)hipFree(a->part_ml);
     (void)hipFree(a->part_acc);
     (void)hipFree(a->st_q);
@@ -481,6 +550,8 @@ extern "C" void janas_attn_destroy(struct janas_attn *a)
             }
             delete v;
         }
+    if (a->part_ev)
+        (void)hipEventDestroy(a->part_ev);
     if (a->stream)
         (void)hipStreamDestroy(a->stream);
     free(a);
@@ -530,6 +601,45 @@ extern "C" int janas_attn_scores_auto(const struct janas_attn *a)
     return a ? a->scores_auto : 0;
 }
 
+namespace {
+
+/* A staging buffer of at least `need` bytes (the stream that used it is
+   synchronized at the end of every janas_attn_run, so the old one is idle). */
+bool staging(void **p, size_t *have, size_t need)
+{
+    if (*p && *have >= need)
+        return true;
+    (void)hipFree(*p);
+    *p = nullptr;
+    *have = 0;
+    if (hipMalloc(p, need) != hipSuccess) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        return false;
+    }
+    *have = need;
+    return true;
+}
+
+/* janas_attn_run's failure: remembered; then an abort (the default), or a
+   return with a host output filled with NaN (the caller is expected to
+   check janas_attn_status and recompute on its own path) */
+void run_failed(janas_attn *a, const char *what, int rc, float *out, size_t qbytes,
+                bool out_host)
+{
+    note(a, rc);
+    if (a->abort_on_error)
+        die(what, rc);
+    fprintf(stderr, "janas_attn_run: %s (%s)\n", what, janas_attn_strerror(rc));
+    if (out && out_host) {
+        const size_t nf = qbytes / sizeof(float);
+        for (size_t i = 0; i < nf; i++)
+            out[i] = NAN;
+    }
+}
+
+}  // namespace
+
 extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
                                const float *q, const int8_t *k,
                                const float *ks, const int8_t *v,
@@ -541,18 +651,30 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
     a->last = nullptr; /* one call only (attention.c:1270-1272) */
     if (n == 0)
         return;
-    if (n > JANAS_ATTN_MAX_BLOCK)
-        die("more tokens than JANAS_ATTN_MAX_BLOCK", JANAS_ATTN_EINVAL);
-    if (hipSetDevice(a->dev) != hipSuccess)
-        die("set device", JANAS_ATTN_EDEVICE);
-    const int kv = a->kv16 ? kI16 : kI8;
-    const size_t eb = elem_bytes(kv), hd = a->hd, cap = a->n_ctx;
+    const size_t hd = a->hd, cap = a->n_ctx;
     const size_t qbytes = (size_t)n * a->n_head * hd * sizeof(float);
+    const bool out_host = !is_device_ptr(out);
+    if (n > JANAS_ATTN_MAX_BLOCK) {
+        run_failed(a, "more tokens than JANAS_ATTN_MAX_BLOCK", JANAS_ATTN_EINVAL, out, qbytes,
+                   out_host);
+        return;
+    }
+    if (hipSetDevice(a->dev) != hipSuccess) {
+        (void)hipGetLastError();
+        run_failed(a, "set device", JANAS_ATTN_EDEVICE, out, qbytes, out_host);
+        return;
+    }
+    const int kv = a->kv16 ? kI16 : kI8;
+    const size_t eb = elem_bytes(kv);
     uint32_t end = last ? last[n - 1] + 1 : pos0 + n;
-    if (!a->ring && end > cap)
-        die("positions past the cache", JANAS_ATTN_ERANGE);
+    if (!a->ring && end > cap) {
+        /* the reference reads past its cache here; a device fault is worse */
+        run_failed(a, "positions past the cache", JANAS_ATTN_ERANGE, out, qbytes, out_host);
+        return;
+    }
     uint32_t c0 = first_chunk(a->window, pos0);
     if (a->ring && ((end + kChunk - 1) / kChunk - c0) * kChunk > cap) {
+        /* attention.c:1281-1286: an abort in the reference too */
         fprintf(stderr, "janas_attn_run: %u chunks for a ring of %u\n",
                 (end + kChunk - 1) / kChunk - c0, (uint32_t)(cap / kChunk));
         abort();
@@ -566,31 +688,33 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
     /* q and out: in place on the device, else through a block's buffer */
     const size_t blk_bytes =
         (size_t)JANAS_ATTN_MAX_BLOCK * a->n_head * hd * sizeof(float);
+    size_t have_q = a->st_q ? blk_bytes : 0, have_out = a->st_out ? blk_bytes : 0;
     if (is_device_ptr(q)) {
         s.q = q;
     } else {
-        if (!a->st_q && hipMalloc(&a->st_q, blk_bytes) != hipSuccess) {
-            (void)hipGetLastError();
-            die("staging q", JANAS_ATTN_ENOMEM);
+        if (!staging((void **)&a->st_q, &have_q, blk_bytes)) {
+            run_failed(a, "staging q", JANAS_ATTN_ENOMEM, out, qbytes, out_host);
+            return;
         }
-        rc = hip_err(hipMemcpyAsync(a->st_q, q, qbytes, hipMemcpyHostToDevice,
-                                    a->stream),
+        rc = hip_err(hipMemcpyAsync(a->st_q, q, qbytes, hipMemcpyHostToDevice, a->stream),
                      "copy q");
-        if (rc)
-            die("staging q", rc);
+        if (rc) {
+            run_failed(a, "staging q", rc, out, qbytes, out_host);
+            return;
+        }
         s.q = a->st_q;
     }
-    const bool out_host = !is_device_ptr(out);
     if (out_host) {
-        if (!a->st_out && hipMalloc(&a->st_out, blk_bytes) != hipSuccess) {
-            (void)hipGetLastError();
-            die("staging out", JANAS_ATTN_ENOMEM);
+        if (!staging((void **)&a->st_out, &have_out, blk_bytes)) {
+            run_failed(a, "staging out", JANAS_ATTN_ENOMEM, out, qbytes, out_host);
+            return;
         }
         s.out = a->st_out;
     } else {
         s.out = out;
     }
-    /* the cache: in place on the device, else the rows this call reads */
+    /* the cache: in place on the device, else the rows this call reads (the
+       staging buffers follow the element size: set_kv16 may change it) */
     const size_t rows_all = (size_t)a->n_kv * cap;
     const size_t kv_bytes = rows_all * hd * eb, sc_bytes = rows_all * 4;
     size_t r_lo = a->ring ? 0 : (size_t)c0 * kChunk;
@@ -598,22 +722,21 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
     struct Src {
         const void *p;
         void **st;
+        size_t *have;
         size_t bytes, esz;
         const void **dst;
-    } src[4] = {{k, &a->st_k, kv_bytes, hd * eb, &s.k},
-                {v, &a->st_v, kv_bytes, hd * eb, &s.v},
-                {ks, (void **)&a->st_ks, sc_bytes, 4, (const void **)&s.ks},
-                {vs, (void **)&a->st_vs, sc_bytes, 4, (const void **)&s.vs}};
+    } src[4] = {{k, &a->st_k, &a->st_k_bytes, kv_bytes, hd * eb, &s.k},
+                {v, &a->st_v, &a->st_v_bytes, kv_bytes, hd * eb, &s.v},
+                {ks, (void **)&a->st_ks, &a->st_ks_bytes, sc_bytes, 4, (const void **)&s.ks},
+                {vs, (void **)&a->st_vs, &a->st_vs_bytes, sc_bytes, 4, (const void **)&s.vs}};
     for (Src &x : src) {
         if (is_device_ptr(x.p)) {
             *x.dst = x.p;
             continue;
         }
-        if (!*x.st) {
-            if (hipMalloc(x.st, x.bytes) != hipSuccess) {
-                (void)hipGetLastError();
-                die("staging the cache", JANAS_ATTN_ENOMEM);
-            }
+        if (!staging(x.st, x.have, x.bytes)) {
+            run_failed(a, "staging the cache", JANAS_ATTN_ENOMEM, out, qbytes, out_host);
+            return;
         }
         /* per KV head, rows r_lo .. r_hi - 1 */
         size_t pitch = cap * x.esz, width = (r_hi - r_lo) * x.esz;
@@ -622,38 +745,63 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
         rc = hip_err(hipMemcpy2DAsync(dp, pitch, sp, pitch, width, a->n_kv,
                                       hipMemcpyHostToDevice, a->stream),
                      "copy cache rows");
-        if (rc)
-            die("staging the cache", rc);
+        if (rc) {
+            run_failed(a, "staging the cache", rc, out, qbytes, out_host);
+            return;
+        }
         *x.dst = *x.st;
     }
     if (last) {
-        if (!a->st_last &&
-            hipMalloc(&a->st_last, JANAS_ATTN_MAX_BLOCK * sizeof(uint32_t)) !=
-                hipSuccess) {
-            (void)hipGetLastError();
-            die("staging last", JANAS_ATTN_ENOMEM);
+        size_t have_last = a->st_last ? JANAS_ATTN_MAX_BLOCK * sizeof(uint32_t) : 0;
+        if (!staging((void **)&a->st_last, &have_last, JANAS_ATTN_MAX_BLOCK * sizeof(uint32_t))) {
+            run_failed(a, "staging last", JANAS_ATTN_ENOMEM, out, qbytes, out_host);
+            return;
         }
         rc = hip_err(hipMemcpyAsync(a->st_last, last, n * sizeof(uint32_t),
                                     hipMemcpyHostToDevice, a->stream),
                      "copy last");
-        if (rc)
-            die("staging last", rc);
+        if (rc) {
+            run_failed(a, "staging last", rc, out, qbytes, out_host);
+            return;
+        }
         s.last = a->st_last;
         s.last_max = last[n - 1];
     }
     rc = run_split(a, kv, kGateNone, &s, 1, a->stream);
-    if (rc)
-        die("attention", rc);
+    if (rc) {
+        (void)hipStreamSynchronize(a->stream);
+        run_failed(a, "attention", rc, out, qbytes, out_host);
+        return;
+    }
     if (out_host) {
-        rc = hip_err(hipMemcpyAsync(out, a->st_out, qbytes,
-                                    hipMemcpyDeviceToHost, a->stream),
+        rc = hip_err(hipMemcpyAsync(out, a->st_out, qbytes, hipMemcpyDeviceToHost, a->stream),
                      "copy out");
-        if (rc)
-            die("copy out", rc);
+        if (rc) {
+            (void)hipStreamSynchronize(a->stream);
+            run_failed(a, "copy out", rc, out, qbytes, out_host);
+            return;
+        }
     }
     rc = hip_err(hipStreamSynchronize(a->stream), "synchronize");
     if (rc)
-        die("synchronize", rc);
+        run_failed(a, "synchronize", rc, out, qbytes, out_host);
+}
+
+extern "C" int janas_attn_status(const struct janas_attn *a)
+{
+    return a ? a->status : JANAS_ATTN_EINVAL;
+}
+
+extern "C" void janas_attn_clear_status(struct janas_attn *a)
+{
+    if (a)
+        a->status = JANAS_ATTN_OK;
+}
+
+extern "C" void janas_attn_set_abort(struct janas_attn *a, int on)
+{
+    if (a)
+        a->abort_on_error = on != 0;
 }
 
 /* ===== Part 2 ========================================================= */
@@ -668,7 +816,7 @@ extern "C" int janas_attn_run_dev_split(struct janas_attn *a, int kv_type,
         return rc;
     hipStream_t st = stream ? (hipStream_t)stream : a->stream;
     rc = run_split(a, kv_type, gate_mode, seqs, n_seqs, st);
-    return rc ? rc : put_q8k(a, seqs, n_seqs, st);
+    return note(a, rc ? rc : put_q8k(a, seqs, n_seqs, st));
 }
 
 extern "C" int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
@@ -681,13 +829,15 @@ extern "C" int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
         return rc;
     hipStream_t st = stream ? (hipStream_t)stream : a->stream;
     rc = run_prefill(a, kv_type, gate_mode, seqs, n_seqs, st);
-    return rc ? rc : put_q8k(a, seqs, n_seqs, st);
+    return note(a, rc ? rc : put_q8k(a, seqs, n_seqs, st));
 }
 
-extern "C" int janas_attn_run_dev(struct janas_attn *a, int kv_type,
-                                  int gate_mode,
-                                  const struct janas_attn_seq *seqs,
-                                  uint32_t n_seqs, void *stream)
+namespace {
+
+/* janas_attn_run_dev's routing; fixed: the partials in the device's fixed
+   array (the allocation-free entry point) */
+int run_dev(janas_attn *a, int kv_type, int gate_mode, const janas_attn_seq *seqs,
+            uint32_t n_seqs, void *stream, bool fixed)
 {
     int rc = check_call(a, kv_type, gate_mode, seqs, n_seqs);
     if (rc)
@@ -699,21 +849,44 @@ extern "C" int janas_attn_run_dev(struct janas_attn *a, int kv_type,
     for (uint32_t i = 0; i < n_seqs; i++)
         any_long |= seqs[i].n > JANAS_ATTN_MAX_BLOCK;
     if (any_long && prefill_supported(kv_type, a->hd)) {
-        std::vector<janas_attn_seq> shortq, longq;
-        for (uint32_t i = 0; i < n_seqs; i++)
-            (seqs[i].n > JANAS_ATTN_MAX_BLOCK ? longq : shortq).push_back(seqs[i]);
-        if (!shortq.empty()) {
-            rc = run_split(a, kv_type, gate_mode, shortq.data(),
-                           (uint32_t)shortq.size(), st);
-            if (rc)
-                return rc;
+        /* at most kMaxSeqs a launch: the split for short, the prefill for
+           long sequences, in the caller's order within each */
+        janas_attn_seq shortq[kMaxSeqs], longq[kMaxSeqs];
+        for (uint32_t s0 = 0; s0 < n_seqs; s0 += kMaxSeqs) {
+            const uint32_t m = std::min(kMaxSeqs, n_seqs - s0);
+            uint32_t ns = 0, nl = 0;
+            for (uint32_t i = 0; i < m; i++) {
+                const janas_attn_seq &q = seqs[s0 + i];
+                if (q.n > JANAS_ATTN_MAX_BLOCK)
+                    longq[nl++] = q;
+                else
+                    shortq[ns++] = q;
+            }
+            if (ns) {
+                rc = run_split(a, kv_type, gate_mode, shortq, ns, st, 3, fixed);
+                if (rc)
+                    return note(a, rc);
+            }
+            if (nl) {
+                rc = run_prefill(a, kv_type, gate_mode, longq, nl, st, fixed);
+                if (rc)
+                    return note(a, rc);
+            }
         }
-        rc = run_prefill(a, kv_type, gate_mode, longq.data(),
-                         (uint32_t)longq.size(), st);
     } else {
-        rc = run_split(a, kv_type, gate_mode, seqs, n_seqs, st);
+        rc = run_split(a, kv_type, gate_mode, seqs, n_seqs, st, 3, fixed);
     }
-    return rc ? rc : put_q8k(a, seqs, n_seqs, st);
+    return note(a, rc ? rc : put_q8k(a, seqs, n_seqs, st));
+}
+
+}  // namespace
+
+extern "C" int janas_attn_run_dev(struct janas_attn *a, int kv_type,
+                                  int gate_mode,
+                                  const struct janas_attn_seq *seqs,
+                                  uint32_t n_seqs, void *stream)
+{
+    return run_dev(a, kv_type, gate_mode, seqs, n_seqs, stream, false);
 }
 
 extern "C" int janas_attn_run_dev_kernels(struct janas_attn *a, int kv_type,
@@ -727,8 +900,8 @@ extern "C" int janas_attn_run_dev_kernels(struct janas_attn *a, int kv_type,
         return rc;
     if (kernels < 1 || kernels > 3)
         return JANAS_ATTN_EINVAL;
-    return run_split(a, kv_type, gate_mode, seqs, n_seqs,
-                     stream ? (hipStream_t)stream : a->stream, kernels);
+    return note(a, run_split(a, kv_type, gate_mode, seqs, n_seqs,
+                             stream ? (hipStream_t)stream : a->stream, kernels));
 }
 
 extern "C" const char *janas_attn_strerror(int err)

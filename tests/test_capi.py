@@ -85,3 +85,13 @@ def test_no_cpu_fallback_when_library_missing(monkeypatch, tmp_path):
     monkeypatch.setattr(at, "LIB_PATH", str(tmp_path / "missing.so"))
     with pytest.raises(ImportError):
         at.lib()
+
+
+def test_status_of_no_instance_is_einval():
+    """janas_attn_status(NULL) reports an argument error; clear and
+    set_abort accept NULL (no device call)."""
+    L = lib()
+    assert L.janas_attn_status(None) == janas_amd.EINVAL
+    L.janas_attn_clear_status(None)
+    L.janas_attn_set_abort(None, 0)
+
