@@ -200,6 +200,21 @@ int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
                                const struct janas_attn_seq *seqs,
                                uint32_t n_seqs, void *stream);
 
+/*
+ * janas_attn_run_dev without any allocation, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid it). No counterpart in the reference. The partials live in one
+ * fixed array of JANAS_ATTN_NOALLOC_BYTES that each GPU holds from the
+ * library's first janas_attn_create on it until the process ends, instead
+ * of the instance's; a call that needs more returns JANAS_ATTN_ERANGE. Calls
+ * that overlap on one GPU (any instance, any stream) share that array and
+ * race: the caller keeps them in order (one stream, or events).
+ */
+#define JANAS_ATTN_NOALLOC_BYTES (64u << 20)
+int janas_attn_run_dev_noalloc(struct janas_attn *a, int kv_type, int gate_mode,
+                               const struct janas_attn_seq *seqs,
+                               uint32_t n_seqs, void *stream);
+
 /* For measurement: the split-KV path's kernels one at a time - kernels 1
    the split kernel alone (partials only), 2 the merge alone (over the
    partials a previous call left), 3 both (janas_attn_run_dev_split). */

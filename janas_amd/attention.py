@@ -91,7 +91,7 @@ def lib():
                                  _u32, _vp]
     L.janas_attn_run.restype = None
     for name in ("janas_attn_run_dev", "janas_attn_run_dev_split",
-                 "janas_attn_run_dev_prefill"):
+                 "janas_attn_run_dev_prefill", "janas_attn_run_dev_noalloc"):
         f = getattr(L, name)
         f.argtypes = [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(Seq),
                       _u32, _vp]
@@ -258,7 +258,8 @@ class Attention:
         else:
             fn = {"auto": lib().janas_attn_run_dev,
                   "split": lib().janas_attn_run_dev_split,
-                  "prefill": lib().janas_attn_run_dev_prefill}[path]
+                  "prefill": lib().janas_attn_run_dev_prefill,
+                  "noalloc": lib().janas_attn_run_dev_noalloc}[path]
 
         def call():
             rc = fn(a, kv_type, gate_mode, arr, n, st)

@@ -229,7 +229,19 @@ struct Parts {
 
 int get_parts(janas_attn *a, uint64_t rows, hipStream_t stream, bool fixed, Parts &p)
 {
-    (void)fixed;
+    if (fixed) {
+        char *base = (char *)scratch_ptr(a->dev);
+        if (!base)
+            return JANAS_ATTN_EDEVICE;
+        /* ml: rows x 2 floats, then acc (256-byte aligned): rows x hd */
+        const uint64_t ml_bytes = (rows * 2 * sizeof(float) + 255) / 256 * 256;
+        if (ml_bytes + rows * a->hd * sizeof(float) > JANAS_ATTN_NOALLOC_BYTES)
+            return JANAS_ATTN_ERANGE;
+        p.ml = (float *)base;
+        p.acc = (float *)(base + ml_bytes);
+        p.fixed = true;
+        return JANAS_ATTN_OK;
+    }
     int rc = ensure_part(a, rows, stream);
     if (!rc)
         rc = part_sync(a, stream);
@@ -502,6 +514,9 @@ extern "C" struct janas_attn *janas_attn_create(uint32_t n_head,
     a->ev_used = new std::vector<ProfEv>();
     a->ev_free = new std::vector<ProfEv>();
     a->abort_on_error = 1;
+    /* the allocation-free entry point's partials on this device (a failure
+       only disables that entry point) */
+    (void)scratch_init(dev);
     /* a blocking stream: the calls that run on it (janas_attn_run, and
        Part 2 with a NULL stream) are ordered after work the caller queued
        on the legacy default stream - row writes, copies - and before what
@@ -887,6 +902,14 @@ extern "C" int janas_attn_run_dev(struct janas_attn *a, int kv_type,
                                   uint32_t n_seqs, void *stream)
 {
     return run_dev(a, kv_type, gate_mode, seqs, n_seqs, stream, false);
+}
+
+extern "C" int janas_attn_run_dev_noalloc(struct janas_attn *a, int kv_type,
+                                          int gate_mode,
+                                          const struct janas_attn_seq *seqs,
+                                          uint32_t n_seqs, void *stream)
+{
+    return run_dev(a, kv_type, gate_mode, seqs, n_seqs, stream, true);
 }
 
 extern "C" int janas_attn_run_dev_kernels(struct janas_attn *a, int kv_type,

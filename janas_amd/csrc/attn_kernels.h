@@ -146,6 +146,12 @@ hipError_t launch_rows(const RowArgs &a, hipStream_t s);
 hipError_t launch_shift(const ShiftArgs &a, hipStream_t s);
 hipError_t launch_q8k(const Q8kArgs &a, hipStream_t s);
 
+/* attn_scratch.hip: the device address of the fixed partials array
+   (JANAS_ATTN_NOALLOC_BYTES) on device dev - scratch_init looks it up once,
+   with dev current; scratch_ptr returns it, or null */
+int scratch_init(int dev);
+void *scratch_ptr(int dev);
+
 /* attn_prefill.hip */
 hipError_t launch_prefill(int kv, const PrefillArgs &a, hipStream_t s);
 int prefill_supported(int kv, uint32_t hd);

@@ -1,0 +1,82 @@
+"""janas_attn_run_dev_noalloc: the same results as janas_attn_run_dev,
+bit for bit, with its partials in the device's fixed array - two calls in
+a row (a long decode, then a smaller block and a prompt chunk whose key
+segments need partials), and a call needing more than the array is refused
+with JANAS_ATTN_ERANGE."""
+import numpy as np
+import pytest
+import torch
+
+import janas_amd
+from cases import normal
+from janas_amd import Attention
+
+pytestmark = pytest.mark.gpu
+
+NOALLOC_BYTES = 64 << 20
+
+
+def dev(x, device):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(device)
+
+
+def both(a, kv, seqs, gate_mode, noalloc_outs):
+    """run_dev into the seqs' outs, then run_dev_noalloc into noalloc_outs
+    (same inputs)."""
+    a.run_dev(kv, seqs, gate_mode=gate_mode)
+    seqs2 = [dict(s, out=o) for s, o in zip(seqs, noalloc_outs)]
+    a.run_dev(kv, seqs2, gate_mode=gate_mode, path="noalloc")
+    torch.cuda.synchronize()
+
+
+def test_noalloc_equals_run_dev_twice(gpu):
+    # call 1: config 4's decode (16 / 2 / 256, 32k positions, gated)
+    h, kvh, hd, L = 16, 2, 256, 32768
+    k = dev(normal(101, kvh * L * hd).reshape(kvh, L, hd).astype(np.float16), gpu)
+    v = dev(normal(103, kvh * L * hd).reshape(kvh, L, hd).astype(np.float16), gpu)
+    q = dev(normal(107, h * hd).reshape(1, h, hd), gpu)
+    g = dev(normal(109, h * hd).reshape(1, h, hd), gpu)
+    out, out2 = torch.empty_like(q), torch.full_like(q, float("nan"))
+    with Attention(h, kvh, hd, L) as a:
+        a.set_scale(1.0 / 16.0)
+        both(a, janas_amd.KV_F16, [dict(k=k, v=v, q=q, out=out, gate=g, cap=L,
+                                        n=1, pos0=L - 1)],
+             janas_amd.GATE_ELEM, [out2])
+    assert torch.equal(out, out2)
+    # call 2, smaller: a 16-token block (split path) and a 512-token chunk
+    # of a prompt at 4096 (prefill path, split into key segments) over an
+    # int8 cache, 32 / 8 / 128
+    h, kvh, hd, L = 32, 8, 128, 4608
+    k8 = np.clip(np.rint(normal(111, kvh * L * hd) * 30), -127, 127).astype(np.int8)
+    v8 = np.clip(np.rint(normal(113, kvh * L * hd) * 30), -127, 127).astype(np.int8)
+    ks = (0.01 + 0.01 * np.abs(normal(117, kvh * L))).astype(np.float32)
+    vs = (0.01 + 0.01 * np.abs(normal(119, kvh * L))).astype(np.float32)
+    kd, vd = dev(k8.reshape(kvh, L, hd), gpu), dev(v8.reshape(kvh, L, hd), gpu)
+    ksd, vsd = dev(ks.reshape(kvh, L), gpu), dev(vs.reshape(kvh, L), gpu)
+    qa = dev(normal(121, 16 * h * hd).reshape(16, h, hd), gpu)
+    qb = dev(normal(123, 512 * h * hd).reshape(512, h, hd), gpu)
+    oa, ob = torch.empty_like(qa), torch.empty_like(qb)
+    oa2, ob2 = torch.full_like(qa, float("nan")), torch.full_like(qb, float("nan"))
+    with Attention(h, kvh, hd, L) as a:
+        both(a, janas_amd.KV_I8,
+             [dict(k=kd, v=vd, ks=ksd, vs=vsd, q=qa, out=oa, cap=L, n=16, pos0=3000),
+              dict(k=kd, v=vd, ks=ksd, vs=vsd, q=qb, out=ob, cap=L, n=512, pos0=4096)],
+             janas_amd.GATE_NONE, [oa2, ob2])
+    assert torch.equal(oa, oa2)
+    assert torch.equal(ob, ob2)
+
+
+def test_noalloc_refuses_more_than_the_array(gpu):
+    """A 64-token block at 32k over 8 KV heads of 128 needs 8 x 128 x 64 x 4
+    partial rows of 130 floats (34 MB) - fits; at 64k it needs twice that."""
+    h, kvh, hd, L = 32, 8, 128, 65536
+    k = torch.zeros((kvh, L, hd), dtype=torch.float16, device=gpu)
+    q = torch.zeros((64, h, hd), dtype=torch.float32, device=gpu)
+    out = torch.empty_like(q)
+    with Attention(h, kvh, hd, L) as a:
+        rows = kvh * (L // 256) * 64 * (h // kvh)
+        assert rows * (hd + 2) * 4 > NOALLOC_BYTES
+        with pytest.raises(janas_amd.AttnError) as e:
+            a.run_dev(janas_amd.KV_F16, [dict(k=k, v=k, q=q, out=out, cap=L,
+                                              n=64, pos0=L - 64)], path="noalloc")
+        assert e.value.code == janas_amd.ERANGE
