@@ -66,6 +66,27 @@ def decode_workload():
                 g=normal(rng, (1, h, hd), np.float32))
 
 
+def quantized(x, dtype):
+    """Rows of x (n_kv, L, hd) quantized as the engine's cache write does
+    (model_attn.c:126-145): the row's largest magnitude becomes 127 or
+    32767, one float scale a row."""
+    top = 127 if dtype == np.int8 else 32767
+    xf = x.astype(np.float32)
+    mx = np.abs(xf).max(axis=2, keepdims=True)
+    mx[mx == 0] = 1.0
+    q = np.rint(xf * (top / mx)).astype(dtype)
+    return q, (mx[..., 0] / top).astype(np.float32)
+
+
+def int_decode_workload(dtype):
+    """BASELINE config 4's shape over the engine's own cache formats: the
+    same N(0, 1) keys and values as int8 or int16 with per-row scales."""
+    w = decode_workload()
+    k, ks = quantized(w["k"], dtype)
+    v, vs = quantized(w["v"], dtype)
+    return dict(w, k=k, v=v, ks=ks, vs=vs)
+
+
 def wide_workload():
     """head_dim 512 over an int16 cache (Gemma 4's full-attention layers):
     keys and values uniform int16, scales U(0.001, 0.02) / 258 as the
@@ -107,10 +128,30 @@ def traffic_from_profiles(kernel):
     return float(m.group(1)) if m else None
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or the platform's."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def cpu_cores():
+    """Every core the host gives this process (all host cores)."""
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        return max(1, os.cpu_count() or 1)
+
+
 def cpu_decode_baseline(w, budget_s=10.0):
     """The restatement on the host's cores over the same config-4 call."""
     from oracle import orc
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores = cpu_cores()
     args = dict(n_head=w["h"], n_kv=w["kvh"], hd=w["hd"], pos0=w["L"] - 1,
                 kv=orc.KV_F16, scale=w["scale"], threads=cores)
     orc.run(w["q"], w["k"], w["v"], **args)  # warm-up
@@ -124,33 +165,44 @@ def cpu_decode_baseline(w, budget_s=10.0):
     t = float(np.median(times))
     kv_bytes = 2 * w["kvh"] * w["L"] * w["hd"] * 2
     return {"value": round(kv_bytes / t / 1e9, 3), "unit": "GB/s",
-            "cores": cores, "kind": "port",
+            "cores": cores, "cpu": cpu_model(), "kind": "port",
             "sample": f"config 4 decode call (32768 positions), median of "
                       f"{len(times)} calls, {t * 1e3:.1f} ms each"}
 
 
-def cpu_prefill_baseline(w, block=64):
-    """The restatement on the host's cores over the prompt's last block of
-    64 tokens (the costliest call of the engine's 64-token prefill)."""
+def cpu_prefill_baseline(w, block=64, every=8):
+    """The restatement on the host's cores over the 8k prompt as the engine
+    makes it: 128 calls of 64 tokens (model_attn.c:343-353). Every
+    every-th call is timed (one each, after one warm-up call) and the
+    prompt's time is their sum times every - a bounded sample: a block's
+    cost grows linearly with its position, so the sampled blocks (positions
+    0, 512, 1024, ...) stand for the 8 blocks after each of them up to half
+    a block's growth, which the report's figure includes."""
     from oracle import orc
-    cores = max(1, min(16, os.cpu_count() or 1))
-    pos0 = w["L"] - block
-    args = dict(n_head=w["h"], n_kv=w["kvh"], hd=w["hd"], pos0=pos0,
-                kv=orc.KV_F16, scale=float(w["scale"]), threads=cores)
-    q = np.ascontiguousarray(w["q"][pos0:])
-    orc.run(q, w["k"], w["v"], **args)  # warm-up
-    times = []
-    for _ in range(3):
+    cores = cpu_cores()
+    L = w["L"]
+    args = dict(n_head=w["h"], n_kv=w["kvh"], hd=w["hd"], kv=orc.KV_F16,
+                scale=float(w["scale"]), threads=cores)
+    q0 = np.ascontiguousarray(w["q"][:block])
+    orc.run(q0, w["k"], w["v"], pos0=0, **args)  # warm-up
+    starts = list(range(0, L, block * every))
+    t = 0.0
+    for p in starts:
+        q = np.ascontiguousarray(w["q"][p:p + block])
         t0 = time.perf_counter()
-        orc.run(q, w["k"], w["v"], **args)
-        times.append(time.perf_counter() - t0)
-    t = float(np.median(times))
-    fl = prefill_flops(w["hd"], w["h"], pos0, block)
-    return {"value": round(fl / t / 1e12, 4), "unit": "TFLOP/s",
-            "cores": cores, "kind": "port",
-            "sample": f"last 64-token block of the 8192-token prompt "
-                      f"(positions {pos0}..{w['L'] - 1}), median of 3 calls, "
-                      f"{t * 1e3:.1f} ms each"}
+        orc.run(q, w["k"], w["v"], pos0=p, **args)
+        t += time.perf_counter() - t0
+    # the sampled block stands for itself and the every - 1 after it; their
+    # work grows by a block each, so scale by the ratio of the work
+    sampled = sum(prefill_flops(w["hd"], w["h"], p, block) for p in starts)
+    t_prompt = t * prefill_flops(w["hd"], w["h"], 0, L) / sampled
+    fl = prefill_flops(w["hd"], w["h"], 0, L)
+    return {"value": round(fl / t_prompt / 1e12, 4), "unit": "TFLOP/s",
+            "cores": cores, "cpu": cpu_model(), "kind": "port",
+            "sample": f"the {L}-token prompt as {L // block} calls of {block} "
+                      f"tokens; {len(starts)} of them timed (every {every}th, "
+                      f"{t:.2f} s) and the prompt's time scaled from them by "
+                      f"the work (flops) of the calls: {t_prompt:.2f} s"}
 
 
 NCOPY = 6  # 6 caches of 67 MB: more than the 256 MB infinity cache
@@ -399,6 +451,29 @@ def wide_leg(torch, jm, steps, warmup):
     }
 
 
+def int_decode_leg(torch, jm, steps, warmup):
+    """Config 4's decode over int8 and int16 caches: the step (split +
+    merge), with the split kernel's own time and HBM rate. Bytes: keys,
+    values and their scales once."""
+    res = {}
+    for name, dtype, kv, ncopy in (("4-int8", np.int8, jm.KV_I8, 8),
+                                   ("4-int16", np.int16, jm.KV_I16, 5)):
+        w = int_decode_workload(dtype)
+        ms, _, split_ms, merge_ms = bench_decode(torch, jm, w, steps, warmup,
+                                                 kv=kv, ncopy=ncopy)
+        b = 2 * w["k"].nbytes + 2 * w["ks"].nbytes
+        res[name] = {"workload": "decode, 16 Q / 2 KV heads, head_dim 256, "
+                                 f"32768 positions, {np.dtype(dtype).name} "
+                                 "K/V with per-row scales, f32 q, gated",
+                     "ms": round(ms, 5), "value": round(b / (ms * 1e-3) / 1e9, 1),
+                     "unit": "GB/s", "kv_bytes": b, "bound": "hbm",
+                     "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "split_us": round(split_ms * 1e3, 3),
+                     "split_frac": round(b / (split_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "merge_us": round(merge_ms * 1e3, 3)}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -407,7 +482,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=("decode", "prefill", "wide", "copy",
-                                       "gemm", "configs"),
+                                       "gemm", "configs", "int"),
                     help="run one leg alone (profiling)")
     ap.add_argument("--prefill-steps", type=int, default=20)
     args = ap.parse_args()
@@ -429,6 +504,10 @@ def main():
         return
     if args.only == "configs":
         print(json.dumps(configs_leg(torch, jm)), flush=True)
+        return
+    if args.only == "int":
+        print(json.dumps(int_decode_leg(torch, jm, args.steps, args.warmup)),
+              flush=True)
         return
     if args.only == "prefill":
         wp = prefill_workload()
@@ -498,6 +577,8 @@ def main():
     line["wide"] = wide_leg(torch, jm, max(1, args.steps // 4),
                             min(args.warmup, 20))
     line["configs"] = configs_leg(torch, jm)
+    line["configs"].update(int_decode_leg(torch, jm, max(1, args.steps // 2),
+                                          min(args.warmup, 20)))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_decode_baseline(w)
         line["prefill"]["cpu_baseline"] = cpu_prefill_baseline(wp)
