@@ -44,11 +44,18 @@ extern "C" {
 /* attention.h:26 - tokens a janas_attn_run call takes */
 #define JANAS_ATTN_MAX_BLOCK 64
 
-/* attention.h:43-47. The device computes every score over the float query
-   (FLOAT, the reference's exact path): INT16 is a CPU instruction-set
-   speed-up, and asking for it gets FLOAT, which janas_attn_scores_mode
-   reports - as the reference itself does where INT16 cannot run
-   (attention.c:965-982, :1061-1066). */
+/* attention.h:43-47. FLOAT: every score over the float query (the
+   reference's exact path). INT16 (int8 caches, head_dim a multiple of 16):
+   the reference's integer way - the query quantized to int16 a row, exact
+   integer scores, the weights quantized to int16 per (chunk, token, head)
+   and exact integer value sums (attention.c:158-193, :820-839,
+   attention_scores.h) - whose scores, weights and chunk sums are the
+   reference's bit for bit. janas_attn_create resolves the asked way as the
+   reference does (attention.c:960-982, the JANAS_ATTN environment variable
+   first): AUTO is INT16 past 16384 positions; head_dim not a multiple of
+   16, or janas_attn_set_kv16(a, 1), makes it FLOAT. The reference's
+   calibration of AUTO (timing both ways on the host CPU, attention.c:1080-
+   1262) has no counterpart: the resolved way holds for every call. */
 enum janas_attn_scores {
     JANAS_ATTN_AUTO = 0,
     JANAS_ATTN_FLOAT = 1,
@@ -169,11 +176,13 @@ struct janas_attn_q8k {
 
 /*
  * Attention of n_seqs sequences on a stream (a hipStream_t; NULL: the
- * instance's own), asynchronous. The instance's geometry, scale, window and
- * ring apply to all. Blocks of up to JANAS_ATTN_MAX_BLOCK tokens a sequence
- * take the split-KV path, whose chunking matches janas_attn_run bit for bit
- * token by token; longer prompts take the MFMA prefill path (causal tiles),
- * equal within the f16 tolerance. A prompt whose row blocks alone would
+ * instance's own), asynchronous. The instance's geometry, scale, window,
+ * ring and scores way (INT16 for int8 caches) apply to all. Blocks of up to
+ * JANAS_ATTN_MAX_BLOCK tokens a sequence take the split-KV path, whose
+ * chunking matches janas_attn_run bit for bit token by token; longer
+ * prompts take the MFMA prefill path (causal tiles, f16 query and weights:
+ * equal within 2e-3 of softmax-normalized outputs) - except int8 caches
+ * under INT16, which stay on the split-KV path at any length. A prompt whose row blocks alone would
  * leave compute units idle (a short prompt, a chunk of a long one) has its
  * key range split into segments, merged in order through the partials; the
  * split depends on the sequence and the device alone, so its result is the
@@ -194,7 +203,8 @@ int janas_attn_run_dev_split(struct janas_attn *a, int kv_type, int gate_mode,
 /* The same, always through the MFMA prefill path: f16, int8 and int16
    caches (the latter two dequantized into f16 as tiles are staged),
    head_dim up to 512 (JANAS_ATTN_ENOTSUP for f32 caches;
-   janas_attn_run_dev then takes the split-KV path). */
+   janas_attn_run_dev then takes the split-KV path). Its arithmetic is the
+   f16 one whatever the instance's scores way. */
 int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
                                int gate_mode,
                                const struct janas_attn_seq *seqs,

@@ -32,6 +32,7 @@ struct ProfEv {
 
 struct janas_attn {
     uint32_t n_head, n_kv, hd, n_ctx, group;
+    int scores;           /* JANAS_ATTN_FLOAT or _INT16, as resolved */
     int scores_auto;
     float scale;
     uint32_t window;
@@ -276,8 +277,10 @@ void prof_end(ProfEv *ev, hipStream_t stream)
         (void)hipEventRecord(ev->b, stream);
 }
 
-int fill_args(const janas_attn *a, SplitArgs &args, int gate_mode, const Parts &p)
+int fill_args(const janas_attn *a, int kv, SplitArgs &args, int gate_mode, const Parts &p)
 {
+    /* the INT16 way exists over int8 caches (attention.c:692, :1061-1066) */
+    args.int16 = kv == kI8 && a->scores == JANAS_ATTN_INT16;
     args.part_ml = p.ml;
     args.part_acc = p.acc;
     args.n_head = a->n_head;
@@ -330,7 +333,7 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
             return rc;
         args.n_seqs = m;
         args.n_wg = wg;
-        fill_args(a, args, gate_mode, pt);
+        fill_args(a, kv, args, gate_mode, pt);
         if (kernels & 1) {
             ProfEv *ev = fixed ? nullptr : prof_begin(a, 0, stream);
             hipError_t e = launch_split(kv, args, stream);
@@ -511,6 +514,14 @@ extern "C" struct janas_attn *janas_attn_create(uint32_t n_head,
     else if (e && !strcmp(e, "auto"))
         scores = JANAS_ATTN_AUTO;
     a->scores_auto = scores == JANAS_ATTN_AUTO;
+    /* attention.c:975-982: sixteen keys at a time, so the INT16 way needs
+       head_dim a multiple of 16; AUTO takes it past 16384 positions */
+    if (head_dim % 16)
+        a->scores = JANAS_ATTN_FLOAT;
+    else if (scores == JANAS_ATTN_FLOAT || scores == JANAS_ATTN_INT16)
+        a->scores = scores;
+    else
+        a->scores = n_ctx > 16384 ? JANAS_ATTN_INT16 : JANAS_ATTN_FLOAT;
     a->ev_used = new std::vector<ProfEv>();
     a->ev_free = new std::vector<ProfEv>();
     a->abort_on_error = 1;
@@ -585,6 +596,9 @@ extern "C" void janas_attn_set_window(struct janas_attn *a, uint32_t window)
 extern "C" void janas_attn_set_kv16(struct janas_attn *a, int on)
 {
     a->kv16 = on != 0;
+    /* attention.c:1061-1066: no integer way over 16-bit keys */
+    if (a->kv16 && a->scores == JANAS_ATTN_INT16)
+        a->scores = JANAS_ATTN_FLOAT;
 }
 
 extern "C" void janas_attn_set_ring(struct janas_attn *a, int on)
@@ -607,8 +621,7 @@ extern "C" void janas_attn_set_last(struct janas_attn *a, const uint32_t *last)
 
 extern "C" int janas_attn_scores_mode(const struct janas_attn *a)
 {
-    (void)a;
-    return JANAS_ATTN_FLOAT;
+    return a ? a->scores : JANAS_ATTN_FLOAT;
 }
 
 extern "C" int janas_attn_scores_auto(const struct janas_attn *a)
@@ -863,7 +876,10 @@ int run_dev(janas_attn *a, int kv_type, int gate_mode, const janas_attn_seq *seq
     bool any_long = false;
     for (uint32_t i = 0; i < n_seqs; i++)
         any_long |= seqs[i].n > JANAS_ATTN_MAX_BLOCK;
-    if (any_long && prefill_supported(kv_type, a->hd)) {
+    /* the INT16 way is the split path's alone: an int8 cache under it
+       stays there at any length */
+    const bool int16 = kv_type == kI8 && a->scores == JANAS_ATTN_INT16;
+    if (any_long && !int16 && prefill_supported(kv_type, a->hd)) {
         /* at most kMaxSeqs a launch: the split for short, the prefill for
            long sequences, in the caller's order within each */
         janas_attn_seq shortq[kMaxSeqs], longq[kMaxSeqs];

@@ -227,6 +227,67 @@ __device__ __forceinline__ float from_x1(float a)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kCut2 = -115.41560327111707f;
 
+/* ---- the reference's INT16 way (int8 caches): every float operation
+   rounds where the reference's does - no multiply-add is fused unless
+   written as one - so the scores, weights and quantized numbers are its
+   own, bit for bit ---- */
+
+/* janas_exp_det (vmath.h:36-52): e^x by the Cephes expf polynomial on
+   x - n ln 2, ln 2 in two parts, 2^n put into the exponent */
+__device__ __forceinline__ float exp_det(float x)
+{
+#pragma clang fp contract(off)
+    x = fminf(fmaxf(x, -88.0f), 88.0f);
+    const float n = __builtin_rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(-n, 0.693359375f, x);
+    r = __builtin_fmaf(-n, -2.12194440e-4f, r);
+    float y = 1.9875691500e-4f;
+    y = __builtin_fmaf(y, r, 1.3981999507e-3f);
+    y = __builtin_fmaf(y, r, 8.3334519073e-3f);
+    y = __builtin_fmaf(y, r, 4.1665795894e-2f);
+    y = __builtin_fmaf(y, r, 1.6666665459e-1f);
+    y = __builtin_fmaf(y, r, 5.0000001201e-1f);
+    y = __builtin_fmaf(y, r * r, r);
+    y = y + 1.0f;
+    return y * __uint_as_float((uint32_t)((int32_t)n + 127) << 23);
+}
+
+/* a score from the exact sums of the query's high (x >> 8) and low
+   (x & 255) planes against int8 keys: the int32 sum, then times the query
+   scale, the score scale and the key scale (attention_scores.h:73-81). The
+   high sum times 256 may pass 2^31 on its own: unsigned, it wraps back
+   into the int32 sum, which the reference's bound keeps below 2^31 */
+__device__ __forceinline__ float q16_score(float hi, float lo, float qsc, float scale,
+                                           float ks)
+{
+#pragma clang fp contract(off)
+    const int32_t s = (int32_t)((uint32_t)(int32_t)hi * 256u + (uint32_t)(int32_t)lo);
+    return (float)s * qsc * scale * ks;
+}
+
+/* a weight (att_weights_ref, attention.c:574-588): 0 below e^-80 of the
+   row's largest score m (finite) and for masked scores (-inf) */
+__device__ __forceinline__ float det_weight(float s, float m)
+{
+#pragma clang fp contract(off)
+    const float d = s - m;
+    return d < -80.0f ? 0.0f : exp_det(d);
+}
+
+/* 32767 / mx, or 0 (quant_worker / att_wquant_ref): a quantization's
+   multiplier */
+__device__ __forceinline__ float q16_inv(float mx)
+{
+    return mx > 0.0f ? 32767.0f / mx : 0.0f;
+}
+
+/* x * inv rounded to the nearest integer, ties to even (lrintf) */
+__device__ __forceinline__ int32_t q16_round(float x, float inv)
+{
+#pragma clang fp contract(off)
+    return (int32_t)__builtin_rintf(x * inv);
+}
+
 __device__ __forceinline__ uint32_t row_lo(const SplitArgs &A, uint32_t pos)
 {
     return A.window && pos + 1 > A.window ? pos + 1 - A.window : 0;

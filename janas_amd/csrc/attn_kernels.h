@@ -61,6 +61,8 @@ struct SplitArgs {
     float scale;
     int ring;
     int gate_mode;
+    int int16;             /* the reference's INT16 scores (int8 caches,
+                              hd a multiple of 16) */
 };
 
 /* The causal MFMA pass over whole prompts (prefill, chunked prefill). */

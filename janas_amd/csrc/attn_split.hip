@@ -123,9 +123,10 @@ template <int D> __device__ __forceinline__ uint32_t slot(uint32_t u, uint32_t r
    every chunk is read by one workgroup (decode): nontemporal loads; the row
    tiles of a block of tokens read a chunk each, and plain loads keep it in
    L2 for them. */
-template <int T, int D, bool NT, bool ONE = false>
+template <int T, int D, bool NT, bool ONE = false, bool Q16 = false>
 __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
 {
+    static_assert(!Q16 || (T == kI8 && D % 16 == 0), "INT16: int8 caches");
     using S = SS<T, D>;
     constexpr int KS = S::KS, NT_ = S::NT, LG = S::LG, DP = S::DP;
     __shared__ __attribute__((aligned(1024))) char sR[kSW * S::REG];
@@ -134,6 +135,7 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
     __shared__ __attribute__((aligned(16))) float sM[kSW][8];
     __shared__ __attribute__((aligned(16))) float sL[kSW][8];
     __shared__ float sPe[kSW];
+    __shared__ float sX[kSW][8];   /* INT16: largest weight x value scale */
     __shared__ float sKs[kSW][kSWP], sVs[kSW][kSWP];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -259,6 +261,22 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
 #pragma unroll
         for (int o2 = 1; o2 < QL; o2 <<= 1)
             mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
+        if constexpr (Q16) {
+            /* INT16: the row as int16 with one scale (quant_worker,
+               attention.c:820-839), planes x >> 8 and x & 255 */
+            const float inv = q16_inv(mx);
+            if (qrow[h] < kTileRows) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int32_t qi = ok && qcol[h] < hd ? q16_round(x[e], inv) : 0;
+                    sQ[2 * qrow[h]][qcol[h] + e] = (_Float16)(qi >> 8);
+                    sQ[2 * qrow[h] + 1][qcol[h] + e] = (_Float16)(qi & 255);
+                }
+                if (qcol[h] == 0)
+                    sQs[qrow[h]] = mx / 32767.0f;
+            }
+            continue;
+        }
         int ex = 0;
         if (mx > 0.0f && mx < INFINITY) {
             frexpf(mx, &ex);
@@ -288,6 +306,7 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
     for (int ks = 0; ks < KS; ks++)
         qb[ks] = *(const h8 *)&sQ[l16][32 * ks + 8 * g];
     const float qs2 = sQs[qr] * A.scale * kLog2e;
+    const float qsc = sQs[qr];
 
     char *const myR = sR + w * S::REG;
     /* the group's 16 B of row `row`, byte cb of the padded row, into the
@@ -362,19 +381,68 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t pl = kSG * s + 4 * g + i, p = p0w + pl;
-            float x = (sa[i] + from_x1(sa[i])) * qs2;
-            if constexpr (S::SCALED)
-                x *= sKs[w][pl];
+            float x;
+            if constexpr (Q16) {
+                /* natural units, the reference's score bit for bit */
+                const float other = from_x1(sa[i]);
+                const bool odd = l16 & 1;
+                x = q16_score(odd ? other : sa[i], odd ? sa[i] : other, qsc, A.scale,
+                              sKs[w][pl]);
+            } else {
+                x = (sa[i] + from_x1(sa[i])) * qs2;
+                if constexpr (S::SCALED)
+                    x *= sKs[w][pl];
+            }
             sv[s][i] = p >= rlo && p <= rhi ? x : -INFINITY;
             m = fmaxf(m, sv[s][i]);
         }
     }
     m = max_x32(max_x16(m));
 
+    h4 pa[kSNG];
+    if constexpr (Q16) {
+        /* INT16: the chunk's largest score over the 4 waves, the weights
+           e^(s - M) times the value scales, their largest over the chunk,
+           and the weights quantized against it to 0 .. 32767, planes
+           w >> 8 and w & 255 (att_weights_ref, att_wquant_ref,
+           attention.c:158-176, :574-588, :761-772) */
+        if (lane < 16 && !(lane & 1))
+            sM[w][lane >> 1] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(sM[0][qr], sM[1][qr]), fmaxf(sM[2][qr], sM[3][qr]));
+        const float mm = m == -INFINITY ? 0.0f : m;
+        float pv[kSNG][4];
+        float lsum = 0.0f, vmx = 0.0f;
+#pragma unroll
+        for (int s = 0; s < kSNG; s++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float wt = det_weight(sv[s][i], mm);
+                lsum += wt;
+                pv[s][i] = wt * sVs[w][kSG * s + 4 * g + i];
+                vmx = fmaxf(vmx, pv[s][i]);
+            }
+        vmx = max_x32(max_x16(vmx));
+        lsum = sum_x32(sum_x16(lsum));
+        if (lane < 16 && !(lane & 1)) {
+            sX[w][lane >> 1] = vmx;
+            sL[w][lane >> 1] = lsum;
+        }
+        __syncthreads();
+        const float inv = q16_inv(fmaxf(fmaxf(sX[0][qr], sX[1][qr]), fmaxf(sX[2][qr], sX[3][qr])));
+#pragma unroll
+        for (int s = 0; s < kSNG; s++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int32_t q = q16_round(pv[s][i], inv);
+                pa[s][i] = (l16 & 1) ? (_Float16)(q & 255) : (_Float16)(q >> 8);
+            }
+    }
+
     /* ---- the wave's softmax (powers of two); the weights' power of two
        puts their largest (times the largest value scale) in [2^12, 2^13) */
     int pe = 13;
-    if constexpr (S::SCALED) {
+    if constexpr (S::SCALED && !Q16) {
         float vm = 0.0f;
 #pragma unroll
         for (int s = 0; s < kSNG; s++)
@@ -387,31 +455,32 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
             frexpf(vm, &ev);
         pe = 13 - ev;
     }
-    const float up = ldexpf(1.0f, pe);
-    const float mm = m == -INFINITY ? 0.0f : m;
-    float lsum = 0.0f;
-    h4 pa[kSNG];
+    if constexpr (!Q16) {
+        const float up = ldexpf(1.0f, pe);
+        const float mm = m == -INFINITY ? 0.0f : m;
+        float lsum = 0.0f;
 #pragma unroll
-    for (int s = 0; s < kSNG; s++)
+        for (int s = 0; s < kSNG; s++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float d = sv[s][i] - mm;
-            const float pw = d >= kCut2 ? __builtin_amdgcn_exp2f(d) : 0.0f;
-            lsum += pw;
-            float pv = pw * up;
-            if constexpr (S::SCALED)
-                pv *= sVs[w][kSG * s + 4 * g + i];
-            _Float16 hi, lo;
-            split_hl(pv, hi, lo);
-            pa[s][i] = (l16 & 1) ? lo : hi;
+            for (int i = 0; i < 4; i++) {
+                const float d = sv[s][i] - mm;
+                const float pw = d >= kCut2 ? __builtin_amdgcn_exp2f(d) : 0.0f;
+                lsum += pw;
+                float pv = pw * up;
+                if constexpr (S::SCALED)
+                    pv *= sVs[w][kSG * s + 4 * g + i];
+                _Float16 hi, lo;
+                split_hl(pv, hi, lo);
+                pa[s][i] = (l16 & 1) ? lo : hi;
+            }
+        lsum = sum_x32(sum_x16(lsum));
+        if (lane < 16 && !(lane & 1)) {
+            sM[w][lane >> 1] = m;
+            sL[w][lane >> 1] = lsum;
         }
-    lsum = sum_x32(sum_x16(lsum));
-    if (lane < 16 && !(lane & 1)) {
-        sM[w][lane >> 1] = m;
-        sL[w][lane >> 1] = lsum;
+        if (lane == 0)
+            sPe[w] = ldexpf(1.0f, -pe);
     }
-    if (lane == 0)
-        sPe[w] = ldexpf(1.0f, -pe);
 
     /* ---- values, a group at a time as its V lands ---- */
     f4 o[NT_];
@@ -470,17 +539,32 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     float2 *mine = (float2 *)myR;
 #pragma unroll
-    for (int t = 0; t < NT_; t++)
-        mine[t * 64 + lane] = make_float2(o[t][0] + o[t][1], o[t][2] + o[t][3]);
+    for (int t = 0; t < NT_; t++) {
+        if constexpr (Q16) {
+            /* exact integer sums, 256 hi + lo as int32 bits (at most 64
+               positions of 32767 x 128: no overflow) */
+            const int32_t a0 = (int32_t)o[t][0] * 256 + (int32_t)o[t][1];
+            const int32_t a1 = (int32_t)o[t][2] * 256 + (int32_t)o[t][3];
+            mine[t * 64 + lane] = make_float2(__int_as_float(a0), __int_as_float(a1));
+        } else {
+            mine[t * 64 + lane] = make_float2(o[t][0] + o[t][1], o[t][2] + o[t][3]);
+        }
+    }
     __syncthreads();
     const uint64_t prow = sq.part0 + ((uint64_t)kvh * sq.span + (c - sq.c0)) * R + r0;
     {
         /* lane jj of a tile: source lanes 2 jj, 2 jj + 1 - tile rows 2 gs,
            2 gs + 1 of columns cs, cs + 1 */
         const uint32_t jj = lane & 31, gs = jj >> 3;
-        float fw[kSW][2];
+        float fw[kSW][2], wsc[2];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
+            if constexpr (Q16) {
+                /* the weights' scale, mx / 32767 (att_wquant_ref) */
+                const uint32_t rr = 2 * gs + h;
+                wsc[h] = fmaxf(fmaxf(sX[0][rr], sX[1][rr]), fmaxf(sX[2][rr], sX[3][rr])) / 32767.0f;
+                continue;
+            }
             float mc = -INFINITY;
 #pragma unroll
             for (int ww = 0; ww < kSW; ww++)
@@ -504,9 +588,18 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
                 part[ww] = ((const f4 *)(sR + ww * S::REG))[t * 32 + jj];
             float res[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                res[i] = (part[0][i] * fw[0][i % 2] + part[1][i] * fw[1][i % 2]) +
-                         (part[2][i] * fw[2][i % 2] + part[3][i] * fw[3][i % 2]);
+            for (int i = 0; i < 4; i++) {
+                if constexpr (Q16) {
+                    /* the chunk's exact int32 sum, then one multiply
+                       (att_values_i16_ref, attention.c:178-193) */
+                    const int32_t acc = (__float_as_int(part[0][i]) + __float_as_int(part[1][i])) +
+                                        (__float_as_int(part[2][i]) + __float_as_int(part[3][i]));
+                    res[i] = (float)acc * wsc[i % 2];
+                } else {
+                    res[i] = (part[0][i] * fw[0][i % 2] + part[1][i] * fw[1][i % 2]) +
+                             (part[2][i] * fw[2][i % 2] + part[3][i] * fw[3][i % 2]);
+                }
+            }
             if (cs < hd) {
                 if (r0 + 2 * gs < R)
                     *(float2 *)&A.part_acc[(prow + 2 * gs) * hd + cs] = make_float2(res[0], res[2]);
@@ -524,8 +617,15 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
 #pragma unroll
         for (int ww = 0; ww < kSW; ww++) {
             const float mw = sM[ww][lane];
-            l[ww] = (mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mc)) * sL[ww][lane];
+            if constexpr (Q16)
+                l[ww] = sL[ww][lane]; /* already against the chunk's M */
+            else
+                l[ww] = (mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mc)) * sL[ww][lane];
         }
+        /* INT16's largest score is in natural units: to powers of two for
+           the merge */
+        if constexpr (Q16)
+            mc *= kLog2e;
         *(float2 *)&A.part_ml[(prow + lane) * 2] = make_float2(mc, (l[0] + l[1]) + (l[2] + l[3]));
     }
 }
@@ -686,6 +786,17 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 template <int T, int D>
 hipError_t launch_t(const SplitArgs &a, hipStream_t s)
 {
+    if constexpr (T == kI8 && D % 16 == 0) {
+        if (a.int16) {
+            if (a.once && a.n_seqs == 1)
+                hipLaunchKernelGGL((split_kernel<T, D, true, true, true>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
+            else if (a.once)
+                hipLaunchKernelGGL((split_kernel<T, D, true, false, true>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
+            else
+                hipLaunchKernelGGL((split_kernel<T, D, false, false, true>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
+            return hipGetLastError();
+        }
+    }
     if (a.once && a.n_seqs == 1)
         hipLaunchKernelGGL((split_kernel<T, D, true, true>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
     else if (a.once)

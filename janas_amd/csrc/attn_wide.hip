@@ -91,10 +91,14 @@ template <int T, int D> struct WShape {
     static constexpr int REGION = kRound * VB / 1024 * kBlk;
 };
 
-/* ONE: a launch of one sequence, its descriptor read at fixed offsets */
-template <int T, int D, int NB, bool ONE = false>
+/* ONE: a launch of one sequence, its descriptor read at fixed offsets.
+   Q16: the reference's INT16 way over an int8 cache (attn_split.hip's
+   split kernel has the same arithmetic): a quantized query, exact integer
+   scores, weights quantized per chunk and exact integer value sums */
+template <int T, int D, int NB, bool ONE = false, bool Q16 = false>
 __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 {
+    static_assert(!Q16 || T == kI8, "INT16: int8 caches");
     using E = Elem<T>;
     using S = WShape<T, D>;
     static_assert(S::UNITS * 1024 == kRound * S::RB, "whole kilobytes a round");
@@ -107,6 +111,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     __shared__ float sKz[kChunk], sVz[kChunk];
     __shared__ float sMax[kWWaves][kRows], sSum[kWWaves][kRows];
     __shared__ float sQs[kRows];
+    __shared__ float sX[kWWaves][kRows];  /* INT16: largest weight x value scale */
     __shared__ uint32_t sLo[kRows], sHi[kRows];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -223,26 +228,45 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 #pragma unroll
         for (int o2 = 1; o2 < 16; o2 <<= 1)
             mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
-        int ex = 0;
-        if (mx > 0.0f && mx < INFINITY) {
-            frexpf(mx, &ex);
-            ex = 14 - ex;
-        }
-        const float up = ldexpf(1.0f, ex);
+        if constexpr (Q16) {
+            /* the row as int16 with one scale (quant_worker,
+               attention.c:820-839): planes x >> 8 and x & 255 */
+            const float inv = q16_inv(mx);
 #pragma unroll
-        for (int i = 0; i < S::QV; i++) {
-            const uint32_t col = 4 * (l16 + 16 * i);
-            const float x[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
+            for (int i = 0; i < S::QV; i++) {
+                const uint32_t col = 4 * (l16 + 16 * i);
+                const float x[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                _Float16 hi, lo;
-                split_hl(qok[i] ? x[e] * up : 0.0f, hi, lo);
-                sQ[0][qrow][col + e] = hi;
-                sQ[1][qrow][col + e] = lo;
+                for (int e = 0; e < 4; e++) {
+                    const int32_t qi = qok[i] ? q16_round(x[e], inv) : 0;
+                    sQ[0][qrow][col + e] = (_Float16)(qi >> 8);
+                    sQ[1][qrow][col + e] = (_Float16)(qi & 255);
+                }
             }
+            if (l16 == 0)
+                sQs[qrow] = mx / 32767.0f;
+        } else {
+            int ex = 0;
+            if (mx > 0.0f && mx < INFINITY) {
+                frexpf(mx, &ex);
+                ex = 14 - ex;
+            }
+            const float up = ldexpf(1.0f, ex);
+#pragma unroll
+            for (int i = 0; i < S::QV; i++) {
+                const uint32_t col = 4 * (l16 + 16 * i);
+                const float x[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    _Float16 hi, lo;
+                    split_hl(qok[i] ? x[e] * up : 0.0f, hi, lo);
+                    sQ[0][qrow][col + e] = hi;
+                    sQ[1][qrow][col + e] = lo;
+                }
+            }
+            if (l16 == 0)
+                sQs[qrow] = ldexpf(1.0f, -ex);
         }
-        if (l16 == 0)
-            sQs[qrow] = ldexpf(1.0f, -ex);
     }
     sKz[tid] = kz;
     sVz[tid] = vz;
@@ -251,6 +275,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     const uint32_t rlo = sLo[l16], rhi = sHi[l16];
     /* scores in powers of two: log2 e folded into the scale */
     const float qs = sQs[l16] * A.scale * kLog2e;
+    const float qsc = sQs[l16];
     /* this lane's positions of round r: 16 r + 4 g16 + i of the wave */
     const uint32_t pl = w * kWPos + 4 * g16;
     char *const reg = sW + (size_t)w * S::REGION;
@@ -260,9 +285,15 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     float m = -INFINITY, lsum = 0.0f;
     int pe = 13;
     f4 o[S::NT];
+    /* INT16: the low weight plane's sums apart (each plane's sums are
+       exact integers in f32; their mix 256 hi + lo would not be) */
+    f4 o2[Q16 ? S::NT : 1];
 #pragma unroll
     for (int t = 0; t < S::NT; t++)
         o[t] = f4{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < (Q16 ? S::NT : 1); t++)
+        o2[t] = f4{0, 0, 0, 0};
 
     /* step s (a compile-time constant): round s into LDS, round s + NB
        asked for, round s computed on */
@@ -323,15 +354,21 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
                 }
             }
             const f4 acc = (sa[0][0] + sa[1][0]) + (sa[0][1] + sa[1][1]);
+            /* INT16: the planes' exact sums apart */
+            const f4 ahi = sa[0][0] + sa[1][0], alo = sa[0][1] + sa[1][1];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t pc = pl + kRound * s + i; /* chunk-relative */
                 const uint32_t p = t0 + pc;
                 float x = -INFINITY;
                 if (active && p >= rlo && p <= rhi && p <= plast) {
-                    x = acc[i] * qs;
-                    if constexpr (S::SCALED)
-                        x *= sKz[pc];
+                    if constexpr (Q16) {
+                        x = q16_score(ahi[i], alo[i], qsc, A.scale, sKz[pc]);
+                    } else {
+                        x = acc[i] * qs;
+                        if constexpr (S::SCALED)
+                            x *= sKz[pc];
+                    }
                 }
                 sv[4 * s + i] = x;
                 m = fmaxf(m, x);
@@ -352,17 +389,61 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
                     else
                         vb[t][0] = x;
                 }
+                if constexpr (Q16) {
 #pragma unroll
-                for (int ap = 0; ap < 2; ap++)
+                    for (int t = 0; t < 8; t++) {
+                        o[t8 + t] = mfma16(pa[r][0], vb[t][0], o[t8 + t]);
+                        o2[t8 + t] = mfma16(pa[r][1], vb[t][0], o2[t8 + t]);
+                    }
+                } else {
 #pragma unroll
-                    for (int vp = 0; vp < S::VP; vp++)
+                    for (int ap = 0; ap < 2; ap++)
 #pragma unroll
-                        for (int t = 0; t < 8; t++)
-                            o[t8 + t] = mfma16(pa[r][ap], vb[t][vp], o[t8 + t]);
+                        for (int vp = 0; vp < S::VP; vp++)
+#pragma unroll
+                            for (int t = 0; t < 8; t++)
+                                o[t8 + t] = mfma16(pa[r][ap], vb[t][vp], o[t8 + t]);
+                }
             }
         }
 
-        if constexpr (s == kRounds - 1) {
+        if constexpr (s == kRounds - 1 && Q16) {
+            /* INT16: the chunk's largest score over the 4 waves, the
+               weights e^(s - M) times the value scales, their largest over
+               the chunk, and the weights quantized against it to
+               0 .. 32767, planes w >> 8 and w & 255 (att_weights_ref,
+               att_wquant_ref, attention.c:158-176, :574-588, :761-772) */
+            m = fmaxf(m, __shfl_xor(m, 16, 64));
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            if (lane < 16)
+                sMax[w][lane] = m;
+            __syncthreads();
+            m = fmaxf(fmaxf(sMax[0][l16], sMax[1][l16]), fmaxf(sMax[2][l16], sMax[3][l16]));
+            const float mm = m == -INFINITY ? 0.0f : m;
+            float pv[4 * kRounds];
+            float vmx = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4 * kRounds; e++) {
+                const float wt = det_weight(sv[e], mm);
+                lsum += wt;
+                pv[e] = wt * sVz[pl + kRound * (e / 4) + e % 4];
+                vmx = fmaxf(vmx, pv[e]);
+            }
+            vmx = fmaxf(vmx, __shfl_xor(vmx, 16, 64));
+            vmx = fmaxf(vmx, __shfl_xor(vmx, 32, 64));
+            lsum += __shfl_xor(lsum, 16, 64);
+            lsum += __shfl_xor(lsum, 32, 64);
+            if (lane < 16)
+                sX[w][lane] = vmx;
+            __syncthreads();
+            const float inv = q16_inv(fmaxf(fmaxf(sX[0][l16], sX[1][l16]), fmaxf(sX[2][l16], sX[3][l16])));
+#pragma unroll
+            for (int e = 0; e < 4 * kRounds; e++) {
+                const int32_t q = q16_round(pv[e], inv);
+                pa[e / 4][0][e % 4] = (_Float16)(q >> 8);
+                pa[e / 4][1][e % 4] = (_Float16)(q & 255);
+            }
+        } else if constexpr (s == kRounds - 1) {
             /* the wave's softmax over its 64 positions, one shot */
             m = fmaxf(m, __shfl_xor(m, 16, 64));
             m = fmaxf(m, __shfl_xor(m, 32, 64));
@@ -415,7 +496,8 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
        2^(m_w - M) (and back to 2^0), then summed over the waves in a fixed
        order, half the column tiles at a time ---- */
     if (lane < 16) {
-        sMax[w][lane] = m;
+        if constexpr (!Q16)
+            sMax[w][lane] = m;  /* INT16: the waves' maxima are there */
         sSum[w][lane] = lsum;
     }
     __syncthreads();
@@ -423,7 +505,15 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 #pragma unroll
     for (int ww = 0; ww < kWWaves; ww++)
         mc = fmaxf(mc, sMax[ww][l16]);
-    {
+    if constexpr (Q16) {
+        /* exact integer sums, 256 hi + lo as int32 bits (at most 64
+           positions of 32767 x 128: no overflow) */
+#pragma unroll
+        for (int t = 0; t < S::NT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                o[t][i] = __int_as_float((int32_t)o[t][i] * 256 + (int32_t)o2[t][i]);
+    } else {
         const float f = (m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mc)) * ldexpf(1.0f, -pe);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -431,6 +521,15 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 #pragma unroll
             for (int t = 0; t < S::NT; t++)
                 o[t][i] *= fi;
+        }
+    }
+    /* INT16: the weights' scale of row 4 g16 + i, mx / 32767 */
+    float wsc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (Q16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t rr = 4 * g16 + i;
+            wsc[i] = fmaxf(fmaxf(sX[0][rr], sX[1][rr]), fmaxf(sX[2][rr], sX[3][rr])) / 32767.0f;
         }
     }
     const uint64_t prow = sq.part0 + ((uint64_t)kvh * sq.span + (c - sq.c0)) * R + r0;
@@ -451,7 +550,19 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 #pragma unroll
             for (int ww = 0; ww < kWWaves; ww++)
                 part[ww] = ((const f4 *)(sW + (size_t)ww * S::REGION))[t * 64 + lane];
-            const f4 sum = (part[0] + part[1]) + (part[2] + part[3]);
+            f4 sum;
+            if constexpr (Q16) {
+                /* the chunk's exact int32 sum, then one multiply
+                   (att_values_i16_ref, attention.c:178-193) */
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int32_t acc = (__float_as_int(part[0][i]) + __float_as_int(part[1][i])) +
+                                        (__float_as_int(part[2][i]) + __float_as_int(part[3][i]));
+                    sum[i] = (float)acc * wsc[i];
+                }
+            } else {
+                sum = (part[0] + part[1]) + (part[2] + part[3]);
+            }
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t row = 4 * g16 + i;
@@ -466,9 +577,14 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 #pragma unroll
         for (int ww = 0; ww < kWWaves; ww++) {
             const float mw = sMax[ww][lane];
-            l += (mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mc)) * sSum[ww][lane];
+            if constexpr (Q16)
+                l += sSum[ww][lane]; /* already against the chunk's M */
+            else
+                l += (mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mc)) * sSum[ww][lane];
         }
-        A.part_ml[(prow + lane) * 2] = mc;
+        /* INT16's largest score is in natural units: to powers of two for
+           the merge */
+        A.part_ml[(prow + lane) * 2] = Q16 ? mc * kLog2e : mc;
         A.part_ml[(prow + lane) * 2 + 1] = l;
     }
 }
@@ -476,6 +592,15 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 template <int T, int D, int NB>
 hipError_t launch_w(const SplitArgs &a, hipStream_t s)
 {
+    if constexpr (T == kI8) {
+        if (a.int16) {
+            if (a.n_seqs == 1)
+                hipLaunchKernelGGL((wide_kernel<T, D, NB, true, true>), dim3(a.n_wg), dim3(256), 0, s, a);
+            else
+                hipLaunchKernelGGL((wide_kernel<T, D, NB, false, true>), dim3(a.n_wg), dim3(256), 0, s, a);
+            return hipGetLastError();
+        }
+    }
     if (a.n_seqs == 1)
         hipLaunchKernelGGL((wide_kernel<T, D, NB, true>), dim3(a.n_wg), dim3(256), 0, s, a);
     else

@@ -98,6 +98,8 @@ struct job {
     float *out;
     uint32_t n, pos0, n_chunks, c0, group;
     float *part; /* n_kv x span x n x group x (hd + 2) */
+    int16_t *qi; /* INT16: the quantized query, n x n_head x hd, or NULL */
+    float *qs;   /* and its scales, n x n_head */
     atomic_uint next;
 };
 
@@ -145,7 +147,45 @@ static float weights(float *row, uint32_t nt, uint32_t vis, float *mx)
 
 struct scratch {
     float *kf, *vf, *sc; /* chunk rows as floats; a row of scores a slot */
+    int16_t *w16;        /* INT16: a slot's quantized weights */
+    float *wsc;          /* and their scale */
 };
+
+/* INT16 (quant_worker, attention.c:820-839): a query row to int16 with one
+   scale, rounded to nearest as lrintf does */
+static void quant_row(const float *src, uint32_t hd, int16_t *dst, float *sc)
+{
+    float mx = 0.0f;
+    for (uint32_t i = 0; i < hd; i++) {
+        float v = src[i] < 0.0f ? -src[i] : src[i];
+        if (v > mx)
+            mx = v;
+    }
+    *sc = mx / 32767.0f;
+    float inv = mx > 0.0f ? 32767.0f / mx : 0.0f;
+    for (uint32_t i = 0; i < hd; i++)
+        dst[i] = (int16_t)lrintf(src[i] * inv);
+}
+
+/* INT16 (att_wquant_ref, attention.c:158-176): a row of weights (value
+   scales folded in, none negative) to 0 .. 32767 with one scale */
+static void quant_weights(const float *row, uint32_t nt, int16_t *w16,
+                          float *sc)
+{
+    float mx = 0.0f;
+    for (uint32_t t = 0; t < nt; t++)
+        if (row[t] > mx)
+            mx = row[t];
+    float inv = mx > 0.0f ? 32767.0f / mx : 0.0f;
+    for (uint32_t t = 0; t < nt; t++)
+        w16[t] = (int16_t)lrintf(row[t] * inv);
+    *sc = mx / 32767.0f;
+}
+
+static int int16_way(const struct orc_attn *A)
+{
+    return A->int16 && A->kv == ORC_KV_I8 && A->hd % 16 == 0;
+}
 
 static void item(struct job *a, uint32_t it, struct scratch *w)
 {
@@ -180,12 +220,26 @@ static void item(struct job *a, uint32_t it, struct scratch *w)
     rows_to_f32(A->kv, a->k, r0, nt, hd, w->kf);
     rows_to_f32(A->kv, a->v, r0, nt, hd, w->vf);
     uint32_t ns = (a->n - jlo) * G;
+    const int i16 = a->qi != NULL;
     /* scores of every slot (token, group head) */
     for (uint32_t sl = 0; sl < ns; sl++) {
         uint32_t j = jlo + sl / G, g = sl % G;
-        const float *qv =
-            a->q + ((size_t)j * A->n_head + (size_t)kvh * G + g) * hd;
+        size_t h = (size_t)j * A->n_head + (size_t)kvh * G + g;
         float *row = w->sc + (size_t)sl * ORC_CHUNK;
+        if (i16) {
+            /* an exact integer sum, then three multiplies
+               (attention_scores.h:73-81) */
+            const int16_t *qv = a->qi + h * hd;
+            const int8_t *K = (const int8_t *)a->k + r0 * hd;
+            for (uint32_t t = 0; t < nt; t++) {
+                int32_t acc = 0;
+                for (uint32_t i = 0; i < hd; i++)
+                    acc += (int32_t)qv[i] * K[(size_t)t * hd + i];
+                row[t] = (float)acc * a->qs[h] * A->scale * ks[t];
+            }
+            continue;
+        }
+        const float *qv = a->q + h * hd;
         for (uint32_t t = 0; t < nt; t++) {
             float s = dot8(qv, w->kf + (size_t)t * hd, hd) * A->scale;
             row[t] = scaled ? s * ks[t] : s;
@@ -212,6 +266,32 @@ static void item(struct job *a, uint32_t it, struct scratch *w)
         if (scaled)
             for (uint32_t t = 0; t < nt; t++)
                 row[t] *= vs[t];
+        if (i16)
+            quant_weights(row, nt, w->w16 + (size_t)sl * ORC_CHUNK,
+                          &w->wsc[sl]);
+    }
+    if (i16) {
+        /* exact integer sums of the int16 weights times the int8 values,
+           then one multiply (att_values_i16_ref, attention.c:178-193) */
+        const int8_t *V = (const int8_t *)a->v + r0 * hd;
+        for (uint32_t sl = 0; sl < ns; sl++) {
+            uint32_t j = jlo + sl / G;
+            float *acc = partial(a, kvh, c, j, sl % G) + 2;
+            if (A->window && a->pos0 + j + 1 > A->window &&
+                a->pos0 + j + 1 - A->window >= t1) {
+                /* a chunk wholly before the token's window: no weights */
+                memset(acc, 0, hd * sizeof(float));
+                continue;
+            }
+            const int16_t *wq = w->w16 + (size_t)sl * ORC_CHUNK;
+            for (uint32_t i = 0; i < hd; i++) {
+                int32_t s32 = 0;
+                for (uint32_t t = 0; t < nt; t++)
+                    s32 += (int32_t)wq[t] * V[(size_t)t * hd + i];
+                acc[i] = (float)s32 * w->wsc[sl];
+            }
+        }
+        return;
     }
     /* values: position by position, fused (attention.c:431-466) */
     for (uint32_t sl = 0; sl < ns; sl++) {
@@ -275,7 +355,9 @@ static void *work(void *arg)
         s.kf = malloc(rows * sizeof(float));
         s.vf = malloc(rows * sizeof(float));
         s.sc = malloc((size_t)a->n * a->group * ORC_CHUNK * sizeof(float));
-        if (!s.kf || !s.vf || !s.sc) {
+        s.w16 = malloc((size_t)a->n * a->group * ORC_CHUNK * sizeof(int16_t));
+        s.wsc = malloc((size_t)a->n * a->group * sizeof(float));
+        if (!s.kf || !s.vf || !s.sc || !s.w16 || !s.wsc) {
             wk->ok = 0;
         } else {
             uint32_t items = A->n_kv * span;
@@ -289,6 +371,8 @@ static void *work(void *arg)
         free(s.kf);
         free(s.vf);
         free(s.sc);
+        free(s.w16);
+        free(s.wsc);
     } else {
         uint32_t items = a->n * A->n_head;
         for (;;) {
@@ -374,10 +458,25 @@ int orc_attn_run(const struct orc_attn *A, const float *q, const void *k,
                     sizeof(float));
     if (!a.part)
         return -1;
+    if (int16_way(A)) {
+        size_t rows = (size_t)n * A->n_head;
+        a.qi = malloc(rows * A->hd * sizeof(int16_t));
+        a.qs = malloc(rows * sizeof(float));
+        if (!a.qi || !a.qs) {
+            free(a.qi);
+            free(a.qs);
+            free(a.part);
+            return -1;
+        }
+        for (size_t r = 0; r < rows; r++)
+            quant_row(q + r * A->hd, A->hd, a.qi + r * A->hd, &a.qs[r]);
+    }
     int rc = run_phase(&a, 0, n_threads);
     if (rc == 0)
         rc = run_phase(&a, 1, n_threads);
     free(a.part);
+    free(a.qi);
+    free(a.qs);
     return rc;
 }
 

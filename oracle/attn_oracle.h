@@ -27,6 +27,19 @@
  *     rounded to float (jmath.c:118-121), adds w * l_c unfused and w * acc_c
  *     fused (quant.c:2419-2431), then multiplies by 1 / sum
  *     (attention.c:870-910).
+ * With int16 set (JANAS_ATTN_INT16 over an int8 cache) the reference's
+ * integer way is followed instead, again bit for bit:
+ *   - each (token, head) query row becomes int16, lrintf(q * 32767 / max|q|),
+ *     with the scale max|q| / 32767 (quant_worker, attention.c:820-839);
+ *   - a score is the exact int32 sum of the int16 query times the int8 key,
+ *     converted to float and multiplied by the query scale, then scale, then
+ *     the key scale (attention_scores.h:22-83);
+ *   - the weights times the value scales are quantized per (chunk, token,
+ *     head) row to 0 .. 32767 with one scale, lrintf(w * 32767 / max w)
+ *     (att_wquant_ref, attention.c:158-176), and the values are the exact
+ *     int32 sums of those against the int8 values, times that scale
+ *     (att_values_i16_ref, attention.c:178-193; attention_scores.h:85-157);
+ *   - the largest score and the sum of weights are those of the float way.
  * The element type of the cache is generic: int8 or int16 with one float
  * scale per (KV head, position) - the reference's own formats
  * (attention.h:7-16, 73-76) - or f16 / f32 without scales, the element types
@@ -53,6 +66,9 @@ struct orc_attn {
     uint32_t window;  /* token p sees p - window + 1 .. p; 0: all */
     int ring;         /* position p in row p mod n_ctx */
     int kv;           /* enum orc_kv */
+    int int16;        /* 1: the reference's INT16 scores (below); taken
+                         only for int8 caches with hd a multiple of 16, as
+                         attention.c:965-982 and :1061-1066 allow it */
 };
 
 /*

@@ -32,7 +32,8 @@ _vp = ctypes.c_void_p
 class _Geom(ctypes.Structure):
     _fields_ = [("n_head", _u32), ("n_kv", _u32), ("hd", _u32),
                 ("n_ctx", _u32), ("scale", ctypes.c_float),
-                ("window", _u32), ("ring", ctypes.c_int), ("kv", ctypes.c_int)]
+                ("window", _u32), ("ring", ctypes.c_int), ("kv", ctypes.c_int),
+                ("int16", ctypes.c_int)]
 
 
 _orc = None
@@ -85,10 +86,11 @@ def _ptr(a):
     return None if a is None else a.ctypes.data
 
 
-def _geom(n_head, n_kv, hd, n_ctx, kv, scale=None, window=0, ring=False):
+def _geom(n_head, n_kv, hd, n_ctx, kv, scale=None, window=0, ring=False,
+          int16=False):
     return _Geom(n_head, n_kv, hd, n_ctx,
                  1.0 / np.sqrt(np.float32(hd)) if scale is None else scale,
-                 window, 1 if ring else 0, kv)
+                 window, 1 if ring else 0, kv, 1 if int16 else 0)
 
 
 def _check_inputs(q, k, v, ks, vs, kv):
@@ -100,14 +102,16 @@ def _check_inputs(q, k, v, ks, vs, kv):
 
 
 def run(q, k, v, ks=None, vs=None, *, n_head, n_kv, hd, pos0, kv,
-        scale=None, window=0, ring=False, last=None, threads=8, block=None):
+        scale=None, window=0, ring=False, last=None, threads=8, block=None,
+        int16=False):
     """The restatement over n = q.shape[0] tokens from pos0. k, v are
     n_kv x n_ctx x hd. block: cut the call into pieces of that many tokens,
-    as the engine does (model_attn.c:343-353); None runs it whole."""
+    as the engine does (model_attn.c:343-353); None runs it whole. int16:
+    the reference's INT16 scores (int8 caches, hd a multiple of 16)."""
     _check_inputs(q, k, v, ks, vs, kv)
     n = q.shape[0]
     n_ctx = k.shape[1]
-    g = _geom(n_head, n_kv, hd, n_ctx, kv, scale, window, ring)
+    g = _geom(n_head, n_kv, hd, n_ctx, kv, scale, window, ring, int16)
     out = np.zeros((n, n_head, hd), np.float32)
     last = None if last is None else np.ascontiguousarray(last, np.uint32)
     step = n if block is None else block
@@ -241,8 +245,11 @@ def cache_shift(k, v, kz, vz, *, keep, drop, n_pos, cs, sn, n_rot,
 
 
 class RefAttention:
-    """The reference's compiled attention, FLOAT scores (the exact path),
-    through its own API: janas_attn_create / set_* / run (attention.h)."""
+    """The reference's compiled attention through its own API:
+    janas_attn_create / set_* / run (attention.h). scores: FLOAT (1, the
+    exact path) or INT16 (2) - never AUTO, whose calibration times the host
+    and writes under the home directory. The JANAS_ATTN environment variable
+    overrides it in the reference (attention.c:965-974): callers clear it."""
 
     _lib = None
 
@@ -276,10 +283,13 @@ class RefAttention:
             cls._lib = lib
         return cls._lib
 
-    def __init__(self, n_head, n_kv, hd, n_ctx, threads=4):
+    def __init__(self, n_head, n_kv, hd, n_ctx, threads=4, scores=1):
+        if scores not in (1, 2):
+            raise ValueError("FLOAT (1) or INT16 (2) only")
         lib = self.lib()
         self.pool = lib.janas_pool_create(threads, None)
-        self.a = lib.janas_attn_create(n_head, n_kv, hd, n_ctx, threads, 1)
+        self.a = lib.janas_attn_create(n_head, n_kv, hd, n_ctx, threads,
+                                       scores)
         if not self.pool or not self.a:
             raise RuntimeError("janas_attn_create failed")
         self.n_head, self.hd = n_head, hd

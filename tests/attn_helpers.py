@@ -14,6 +14,22 @@ TOL_F16_ABS = 2e-3   # f16 K/V paths: max |err| on softmax-normalised outputs
 TOL_FLOAT_ABS = 1e-5  # int8 / int16 cache, FLOAT scores (test_attention.c:146)
 
 
+# every parity check of the session: (test, what, achieved error, bar);
+# conftest.py writes them out when JANAS_PARITY_OUT names a file
+MARGINS = []
+
+
+def within(err, bar, what=""):
+    """Record a parity check's achieved error next to its bar (and print
+    it); True when the error is within the bar."""
+    test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    err, bar = float(err), float(bar)
+    MARGINS.append((test, what, err, bar))
+    print(f"{test} {what}: error {err:.3e}, bar {bar:.1e} "
+          f"({err / bar:.1%} of it)")
+    return err <= bar
+
+
 def threads():
     return max(1, min(16, os.cpu_count() or 1))
 

@@ -21,3 +21,22 @@ def gpu():
     assert torch.cuda.is_available(), "GPU test run without a GPU"
     torch.cuda.init()
     return torch.device("cuda:0")
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """With JANAS_PARITY_OUT set: every parity check's achieved error next
+    to its bar, as a markdown table (attn_helpers.within records them)."""
+    path = os.environ.get("JANAS_PARITY_OUT")
+    if not path:
+        return
+    import attn_helpers
+    rows = attn_helpers.MARGINS
+    if not rows:
+        return
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    with open(path, "w") as f:
+        f.write("| test | check | max error | bar | error / bar |\n")
+        f.write("|---|---|---|---|---|\n")
+        for test, what, err, bar in rows:
+            f.write(f"| {test} | {what} | {err:.3e} | {bar:.1e} | "
+                    f"{err / bar:.1%} |\n")

@@ -82,6 +82,13 @@ CASES = {
     "i8_4x2x64_p200_n100_both": dict(n_head=4, n_kv=2, hd=64, n_ctx=300,
                                      pos0=200, n=100, kv=KV_I8,
                                      picture=(230, 290)),
+    # the reference test's own geometry, 16/2/256, across a chunk boundary
+    # (test_attention.c:347-350)
+    "i8_16x2x256_p254_n5": dict(n_head=16, n_kv=2, hd=256, n_ctx=259,
+                                pos0=254, n=5, kv=KV_I8),
+    # head size 512 over an eight-bit cache
+    "i8_2x1x512_p300_n3": dict(n_head=2, n_kv=1, hd=512, n_ctx=303,
+                               pos0=300, n=3, kv=KV_I8),
     # unit scales and integer keys: the float element types' pin
     "i8unit_8x2x128_p300_n4": dict(n_head=8, n_kv=2, hd=128, n_ctx=304,
                                    pos0=300, n=4, kv=KV_I8, unit=True),
@@ -137,6 +144,13 @@ def digest(inputs):
         if a is not None:
             h.update(np.ascontiguousarray(a).tobytes())
     return h.hexdigest()
+
+
+def int16_case(name):
+    """The reference's INT16 scores apply: an int8 cache, head size a
+    multiple of 16 (attention.c:975-977, :1061-1066)."""
+    c = CASES[name]
+    return c["kv"] == KV_I8 and c["hd"] % 16 == 0
 
 
 def call_kwargs(name):

@@ -10,9 +10,11 @@ For every case of cases.py it drives oracle/_ref/libjanas_ref_attn.so -
 reference's API with FLOAT scores (the exact path; no calibration, nothing
 written under ~/.cache), in calls of at most 64 tokens as the engine makes
 them (model_attn.c:284-294), and stores the outputs with a digest of the
-inputs in tests/golden/<case>.npz. It also checks on the way that the block
-equals token-by-token calls bit for bit (attention.h:13-16), as the
-reference's test does.
+inputs in tests/golden/<case>.npz. Where the reference's INT16 scores apply
+(an int8 cache, head size a multiple of 16) the same calls are made again
+with INT16 asked for, into the key out_int16. It also checks on the way that
+the block equals token-by-token calls bit for bit (attention.h:13-16), as
+the reference's test does.
 """
 import os
 import sys
@@ -25,18 +27,21 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, HERE)
 
-from cases import CASES, KV_I16, digest, make_inputs  # noqa: E402
+from cases import CASES, KV_I16, digest, int16_case, make_inputs  # noqa: E402
 
 from oracle import orc  # noqa: E402
 
 MAX_BLOCK = 64  # JANAS_ATTN_MAX_BLOCK, attention.h:26
 
 
-def reference_outputs(name, inp):
+def reference_outputs(name, inp, scores=1):
     c = CASES[name]
-    ra = orc.RefAttention(c["n_head"], c["n_kv"], c["hd"], c["n_ctx"], 4)
+    ra = orc.RefAttention(c["n_head"], c["n_kv"], c["hd"], c["n_ctx"], 4,
+                          scores)
     lib = ra.lib()
     try:
+        if lib.janas_attn_scores_mode(ra.a) != scores:
+            raise AssertionError(f"{name}: scores mode not taken")
         if c["kv"] == KV_I16:
             lib.janas_attn_set_kv16(ra.a, 1)
         if c.get("window"):
@@ -67,15 +72,21 @@ def reference_outputs(name, inp):
 
 
 def main():
-    os.environ["JANAS_ATTN"] = "float"
+    # the mode is asked for at create; the variable would override it
+    os.environ.pop("JANAS_ATTN", None)
     os.environ["HOME"] = tempfile.mkdtemp()
     os.environ.pop("XDG_CACHE_HOME", None)
     for name in CASES:
         inp = make_inputs(name)
         out = reference_outputs(name, inp)
+        extra = {}
+        if int16_case(name):
+            extra["out_int16"] = reference_outputs(name, inp, scores=2)
         path = os.path.join(HERE, name + ".npz")
-        np.savez_compressed(path, out=out, digest=np.array(digest(inp)))
-        print(f"{name}: {out.shape} -> {os.path.relpath(path, ROOT)}")
+        np.savez_compressed(path, out=out, digest=np.array(digest(inp)),
+                            **extra)
+        print(f"{name}: {out.shape}{' +int16' if extra else ''} -> "
+              f"{os.path.relpath(path, ROOT)}")
 
 
 if __name__ == "__main__":

@@ -21,7 +21,7 @@ import pytest
 import torch
 
 import janas_amd as jm
-from attn_helpers import KV_F16, TOL_F16_ABS, TOL_FLOAT_ABS, abs_err, threads
+from attn_helpers import KV_F16, TOL_F16_ABS, TOL_FLOAT_ABS, abs_err, threads, within
 from oracle import orc
 
 pytestmark = pytest.mark.gpu
@@ -244,7 +244,7 @@ def test_q8k_output_bitwise(gpu, path, gate_mode):
                   threads=threads(), block=64)
     if gate_mode:
         orc.gate(ref, g)
-    assert abs_err(o, ref) <= TOL_F16_ABS
+    assert within(abs_err(o, ref), TOL_F16_ABS, "abs_err(o, ref)")
 
 
 def test_q8k_output_needs_whole_blocks(gpu):
@@ -291,4 +291,4 @@ def test_written_cache_attends_like_the_reference(gpu, kv):
         torch.cuda.synchronize()
     ref = orc.run(q, kc, vc, kz, vz, n_head=h, n_kv=kvh, hd=hd,
                   pos0=npos - 4, kv=kv, threads=threads())
-    assert abs_err(out.cpu().numpy(), ref) <= TOL_FLOAT_ABS
+    assert within(abs_err(out.cpu().numpy(), ref), TOL_FLOAT_ABS, "abs_err(out.cpu().numpy(), ref)")

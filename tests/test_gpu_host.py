@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import janas_amd
-from attn_helpers import TOL_FLOAT_ABS, abs_err, threads
+from attn_helpers import TOL_FLOAT_ABS, abs_err, threads, within
 from cases import normal
 from janas_amd import Attention
 from oracle import orc
@@ -54,8 +54,8 @@ def test_staging_follows_kv16_toggle(gpu):
         assert a.status() == 0
     ref8 = reference(q, k8, ks8, v8, vs8, orc.KV_I8, pos0, h, n_kv, hd)
     ref16 = reference(q, k16, ks16, v16, vs16, orc.KV_I16, pos0, h, n_kv, hd)
-    assert abs_err(out8, ref8) <= TOL_FLOAT_ABS
-    assert abs_err(out16, ref16) <= TOL_FLOAT_ABS
+    assert within(abs_err(out8, ref8), TOL_FLOAT_ABS, "abs_err(out8, ref8)")
+    assert within(abs_err(out16, ref16), TOL_FLOAT_ABS, "abs_err(out16, ref16)")
     assert np.array_equal(out8, out8b)
 
 
@@ -126,6 +126,6 @@ def test_run_returns_instead_of_abort(gpu):
         out = np.zeros_like(q)
         a.run(q, k, ks, v, vs, 2, 100, out)
         ref = reference(q, k, ks, v, vs, orc.KV_I8, 100, h, n_kv, hd)
-        assert abs_err(out, ref) <= TOL_FLOAT_ABS
+        assert within(abs_err(out, ref), TOL_FLOAT_ABS, "abs_err(out, ref)")
         a.clear_status()
         assert a.status() == 0

@@ -1,0 +1,262 @@
+"""The reference's INT16 scores way on the GPU (int8 caches, head size a
+multiple of 16): the quantized query, exact integer scores, weights
+quantized per (chunk, token, head) and exact integer value sums
+(attention.c:158-193, :820-839, attention_scores.h).
+
+* janas_attn_create resolves the asked way as the reference's scores_choice
+  does (attention.c:960-982), set_kv16 takes INT16 back to FLOAT
+  (:1061-1066), and janas_attn_scores_mode reports it;
+* the drop-in's outputs against the reference's own INT16 outputs (golden
+  fixtures from its compiled attention) at the FLOAT bar - the scores,
+  weights and chunk sums are the reference's bit for bit, so only the
+  merge's float rounding differs - and against the double-precision
+  closed form at the reference's INT16 bar (test_attention.c:143-148);
+* a block equals its tokens one by one, bit for bit;
+* config 4's geometry at 32k positions (AUTO resolves to INT16 there), the
+  wide kernel's head sizes, windows, rings and last[], against the
+  restatement's INT16 way.
+"""
+import numpy as np
+import pytest
+import torch
+
+import janas_amd
+from attn_helpers import TOL_FLOAT_ABS, abs_err, threads, within
+from cases import CASES, call_kwargs, int16_case, make_inputs, normal, splitmix
+from janas_amd import Attention
+from oracle import orc
+
+pytestmark = pytest.mark.gpu
+
+MAX_BLOCK = janas_amd.MAX_BLOCK
+INT16_CASES = sorted(n for n in CASES if int16_case(n))
+# the reference's bar for its INT16 way against the closed form, absolute on
+# outputs of order one (test_attention.c:143-148)
+TOL_INT16_EXACT = 1e-3
+
+
+def to_dev(x, device):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(device)
+
+
+def make_attn(name, scores=janas_amd.INT16):
+    c = CASES[name]
+    a = Attention(c["n_head"], c["n_kv"], c["hd"], c["n_ctx"], 1, scores)
+    if c.get("window"):
+        a.set_window(c["window"])
+    if c.get("ring"):
+        a.set_ring(True)
+    if c.get("scale") is not None:
+        a.set_scale(c["scale"])
+    return a
+
+
+def run_dropin(name, inp, device=None):
+    """janas_attn_run under INT16 in calls of at most 64 tokens, as the
+    engine makes them; host arrays, or device tensors."""
+    c = CASES[name]
+    n, pos0 = c["n"], c["pos0"]
+    q, k, v, ks, vs, last = (inp[x] for x in ("q", "k", "v", "ks", "vs",
+                                              "last"))
+    out = np.zeros_like(q)
+    if device is not None:
+        q, k, v, ks, vs = (to_dev(x, device) for x in (q, k, v, ks, vs))
+        outd = torch.zeros(out.shape, dtype=torch.float32, device=device)
+    with make_attn(name) as a:
+        assert a.scores_mode() == janas_amd.INT16
+        for s in range(0, n, MAX_BLOCK):
+            m = min(MAX_BLOCK, n - s)
+            if last is not None:
+                a.set_last(np.ascontiguousarray(last[s:s + m]))
+            if device is None:
+                o = np.zeros((m,) + q.shape[1:], np.float32)
+                a.run(np.ascontiguousarray(q[s:s + m]), k, ks, v, vs, m,
+                      pos0 + s, o)
+                out[s:s + m] = o
+            else:
+                a.run(q[s:s + m], k, ks, v, vs, m, pos0 + s, outd[s:s + m])
+        assert a.status() == 0
+    if device is not None:
+        out = outd.cpu().numpy()
+    return out
+
+
+def test_scores_mode_resolution(gpu, monkeypatch):
+    """scores_choice (attention.c:960-982): FLOAT and INT16 as asked, AUTO
+    INT16 past 16384 positions, FLOAT for head sizes not a multiple of 16;
+    the environment variable first; set_kv16 (attention.c:1061-1066)."""
+    monkeypatch.delenv("JANAS_ATTN", raising=False)
+    F, I, A = janas_amd.FLOAT, janas_amd.INT16, janas_amd.AUTO
+    # (asked, head_dim, n_ctx) -> (scores_mode, scores_auto); an unknown
+    # value takes AUTO's rule without being AUTO, as in the reference
+    want = [((F, 128, 1024), (F, 0)), ((I, 128, 1024), (I, 0)),
+            ((A, 128, 16384), (F, 1)), ((A, 128, 16385), (I, 1)),
+            ((I, 40, 1024), (F, 0)), ((A, 40, 32768), (F, 1)),
+            ((I, 512, 1024), (I, 0)), ((7, 128, 32768), (I, 0))]
+    for (scores, hd, n_ctx), got in want:
+        with Attention(4, 2, hd, n_ctx, 1, scores) as a:
+            assert (a.scores_mode(), a.scores_auto()) == got, (scores, hd, n_ctx)
+    with Attention(4, 2, 128, 1024, 1, I) as a:
+        a.set_kv16(True)
+        assert a.scores_mode() == F
+        a.set_kv16(False)
+        assert a.scores_mode() == F   # as the reference: it stays FLOAT
+    monkeypatch.setenv("JANAS_ATTN", "int16")
+    with Attention(4, 2, 128, 1024, 1, F) as a:
+        assert (a.scores_mode(), a.scores_auto()) == (I, 0)
+    monkeypatch.setenv("JANAS_ATTN", "auto")
+    with Attention(4, 2, 128, 32768, 1, F) as a:
+        assert (a.scores_mode(), a.scores_auto()) == (I, 1)
+    monkeypatch.setenv("JANAS_ATTN", "float")
+    with Attention(4, 2, 128, 32768, 1, I) as a:
+        assert (a.scores_mode(), a.scores_auto()) == (F, 0)
+
+
+@pytest.mark.parametrize("name", INT16_CASES)
+def test_int16_dropin_matches_reference(name, gpu):
+    """Host pointers: the reference's own INT16 outputs within the FLOAT
+    bar, the closed form within the reference's INT16 bar."""
+    inp = make_inputs(name)
+    ref = np.load(f"tests/golden/{name}.npz")["out_int16"]
+    out = run_dropin(name, inp)
+    bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+    assert within(abs_err(out, ref), bar, f"{name} int16 vs reference int16")
+    ex = orc.exact(inp["q"], inp["k"], inp["v"], inp["ks"], inp["vs"],
+                   last=inp["last"], **call_kwargs(name))
+    bar = TOL_INT16_EXACT * max(1.0, float(np.abs(ex).max()))
+    assert within(abs_err(out, ex), bar, f"{name} int16 vs closed form")
+
+
+@pytest.mark.parametrize("name", ["i8_8x1x128_p250_n17", "i8_4x2x64_p0_n64",
+                                  "i8_4x1x64_p600_n8_w300",
+                                  "i8_16x2x256_p254_n5", "i8_2x1x512_p300_n3"])
+def test_int16_dropin_device_block_equals_tokens(name, gpu):
+    """Device pointers; a block equals its tokens one by one, bit for bit,
+    and the reference's INT16 outputs within the FLOAT bar."""
+    c = CASES[name]
+    inp = make_inputs(name)
+    ref = np.load(f"tests/golden/{name}.npz")["out_int16"]
+    out = run_dropin(name, inp, device=gpu)
+    bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+    assert within(abs_err(out, ref), bar, f"{name} int16 device")
+    q, k, v, ks, vs = (to_dev(inp[x], gpu) for x in ("q", "k", "v", "ks", "vs"))
+    n, pos0 = c["n"], c["pos0"]
+    blk = torch.zeros(q.shape, dtype=torch.float32, device=gpu)
+    one = torch.zeros(q.shape, dtype=torch.float32, device=gpu)
+    with make_attn(name) as a:
+        for s in range(0, n, MAX_BLOCK):
+            m = min(MAX_BLOCK, n - s)
+            a.run(q[s:s + m], k, ks, v, vs, m, pos0 + s, blk[s:s + m])
+        for j in range(n):
+            a.run(q[j:j + 1], k, ks, v, vs, 1, pos0 + j, one[j:j + 1])
+    assert torch.equal(blk.view(torch.int32), one.view(torch.int32))
+
+
+def int8_cache(seed, n_kv, cap, hd):
+    """Rows of N(0, 1) numbers quantized as the engine writes them (the
+    largest magnitude of a row to 127, model_attn.c:126-145)."""
+    x = normal(seed, n_kv * cap * hd).reshape(n_kv, cap, hd)
+    mx = np.abs(x).max(axis=2, keepdims=True)
+    return (np.rint(x * (127.0 / mx)).astype(np.int8),
+            (mx[..., 0] / 127.0).astype(np.float32))
+
+
+def test_int16_config4_geometry_at_32k(gpu):
+    """16/2/256 over 32768 int8 positions: AUTO resolves to INT16 at this
+    size; one decode token and a 5-token block against the restatement's
+    INT16 way."""
+    h, kvh, hd, L = 16, 2, 256, 32768
+    k, ks = int8_cache(501, kvh, L, hd)
+    v, vs = int8_cache(502, kvh, L, hd)
+    q = normal(503, 5 * h * hd).reshape(5, h, hd)
+    kd, vd, ksd, vsd = (to_dev(x, gpu) for x in (k, v, ks, vs))
+    with Attention(h, kvh, hd, L) as a:
+        assert a.scores_mode() == janas_amd.INT16
+        a.set_scale(1.0 / 16.0)
+        for n in (1, 5):
+            pos0 = L - n
+            qd = to_dev(q[:n], gpu)
+            out = torch.zeros(qd.shape, dtype=torch.float32, device=gpu)
+            a.run(qd, kd, ksd, vd, vsd, n, pos0, out)
+            ref = orc.run(np.ascontiguousarray(q[:n]), k, v, ks, vs,
+                          n_head=h, n_kv=kvh, hd=hd, pos0=pos0, kv=orc.KV_I8,
+                          scale=np.float32(1.0 / 16.0), int16=True,
+                          threads=threads())
+            bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+            assert within(abs_err(out.cpu().numpy(), ref), bar,
+                          f"32k n={n} int16")
+
+
+def draw(i):
+    """Case i's geometry, from the counter generator: head sizes of both
+    kernels (the split kernel to 256, the wide one above), windows, rings,
+    spans that see past themselves."""
+    z = [int(x) for x in splitmix(9300 + i, 12)]
+    hd = [16, 64, 96, 128, 192, 256, 320, 512][z[0] % 8]
+    group = [1, 2, 3, 4, 8][z[1] % 5]
+    n_kv = 1 + z[2] % 2
+    n = 1 + z[3] % 64
+    pos0 = z[4] % 2500
+    window = 0 if z[5] % 2 else 64 + z[6] % 1200
+    ring = window > 0 and z[7] % 3 == 0
+    picture = z[8] % 4 == 0 and n > 4
+    cap = (256 * ((window + n) // 256 + 3) if ring else pos0 + n + z[9] % 300)
+    return dict(hd=hd, n_head=group * n_kv, n_kv=n_kv, n=n, pos0=pos0,
+                window=window, ring=ring, picture=picture, cap=cap,
+                seed=9400 + 10 * i)
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_int16_random_geometries(i, gpu):
+    g = draw(i)
+    h, kvh, hd, cap, n, pos0 = (g[x] for x in ("n_head", "n_kv", "hd", "cap",
+                                               "n", "pos0"))
+    k, ks = int8_cache(g["seed"] + 1, kvh, cap, hd)
+    v, vs = int8_cache(g["seed"] + 2, kvh, cap, hd)
+    q = normal(g["seed"] + 3, n * h * hd).reshape(n, h, hd)
+    last = None
+    if g["picture"]:
+        p = pos0 + np.arange(n)
+        a0, a1 = pos0 + 1, pos0 + n // 2
+        last = np.where((p >= a0) & (p < a1), a1 - 1, p).astype(np.uint32)
+    print(f"case {i}: {g}", flush=True)
+    out = np.zeros_like(q)
+    with Attention(h, kvh, hd, cap, 1, janas_amd.INT16) as a:
+        assert a.scores_mode() == janas_amd.INT16
+        if g["window"]:
+            a.set_window(g["window"])
+        if g["ring"]:
+            a.set_ring(True)
+        if last is not None:
+            a.set_last(last)
+        a.run(q, k, ks, v, vs, n, pos0, out)
+        assert a.status() == 0
+    ref = orc.run(q, k, v, ks, vs, n_head=h, n_kv=kvh, hd=hd, pos0=pos0,
+                  kv=orc.KV_I8, window=g["window"], ring=g["ring"], last=last,
+                  int16=True, threads=threads())
+    bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+    assert within(abs_err(out, ref), bar, f"random {i} int16")
+
+
+def test_int16_run_dev_long_prompt_stays_split(gpu):
+    """run_dev with an int8 cache under INT16: a 200-token prompt stays on
+    the split-KV path (the INT16 way is its alone) - equal to
+    run_dev_split bit for bit - and within the FLOAT bar of the
+    restatement's INT16 way."""
+    h, kvh, hd, cap, n = 8, 2, 128, 1200, 200
+    k, ks = int8_cache(601, kvh, cap, hd)
+    v, vs = int8_cache(602, kvh, cap, hd)
+    q = normal(603, n * h * hd).reshape(n, h, hd)
+    d = dict(k=to_dev(k, gpu), v=to_dev(v, gpu), ks=to_dev(ks, gpu),
+             vs=to_dev(vs, gpu), q=to_dev(q, gpu), cap=cap, n=n, pos0=900)
+    auto = torch.zeros(d["q"].shape, dtype=torch.float32, device=gpu)
+    split = torch.zeros_like(auto)
+    with Attention(h, kvh, hd, cap, 1, janas_amd.INT16) as a:
+        a.run_dev(janas_amd.KV_I8, [dict(d, out=auto)])
+        a.run_dev(janas_amd.KV_I8, [dict(d, out=split)], path="split")
+        torch.cuda.synchronize()
+    assert torch.equal(auto.view(torch.int32), split.view(torch.int32))
+    ref = orc.run(q, k, v, ks, vs, n_head=h, n_kv=kvh, hd=hd, pos0=900,
+                  kv=orc.KV_I8, int16=True, threads=threads())
+    bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+    assert within(abs_err(auto.cpu().numpy(), ref), bar, "200-token int16")

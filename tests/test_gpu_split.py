@@ -9,7 +9,7 @@ import torch
 
 import janas_amd
 from attn_helpers import (KV_F16, KV_F32, KV_I8, TOL_F16_ABS, TOL_F32_REL,
-                          TOL_FLOAT_ABS, abs_err, config, oracle_out, rel_err)
+                          TOL_FLOAT_ABS, abs_err, config, oracle_out, rel_err, within)
 from cases import CASES, KV_I16, call_kwargs, make_inputs
 from janas_amd import Attention
 from oracle import orc
@@ -76,7 +76,7 @@ def test_dropin_host_matches_reference(name, gpu):
     bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
     err = abs_err(out, ref)
     print(f"{name}: |gpu - reference| = {err:.2e} (bar {bar:.1e})")
-    assert err <= bar
+    assert within(err, bar, "vs oracle")
 
 
 @pytest.mark.parametrize("name", SUPPORTED)
@@ -88,7 +88,7 @@ def test_dropin_device_matches_closed_form(name, gpu):
     bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ex).max()))
     err = abs_err(out, ex)
     print(f"{name}: |gpu - exact| = {err:.2e} (bar {bar:.1e})")
-    assert err <= bar
+    assert within(err, bar, "vs oracle")
 
 
 @pytest.mark.parametrize("name", ["i8_8x1x128_p250_n17", "i8_4x2x64_p0_n64",
@@ -138,7 +138,7 @@ def test_config1_f32_decode(gpu):
     ref = oracle_out(orc, cfg, cfg["seqs"][0])
     err = rel_err(out, ref)
     print(f"config 1: max rel err {err:.2e}")
-    assert err <= TOL_F32_REL
+    assert within(err, TOL_F32_REL, "vs oracle")
 
 
 def test_config3_ragged_decode(gpu):
@@ -149,7 +149,7 @@ def test_config3_ragged_decode(gpu):
         worst = max(worst, abs_err(out, oracle_out(orc, cfg, s)))
     print(f"config 3: lens {[s['pos0'] + 1 for s in cfg['seqs']]}, "
           f"max abs err {worst:.2e}")
-    assert worst <= TOL_F16_ABS
+    assert within(worst, TOL_F16_ABS, "worst vs oracle")
 
 
 def test_config4_gated_long_decode(gpu):
@@ -158,7 +158,7 @@ def test_config4_gated_long_decode(gpu):
     ref = oracle_out(orc, cfg, cfg["seqs"][0])
     err = abs_err(out, ref)
     print(f"config 4: max abs err {err:.2e}")
-    assert err <= TOL_F16_ABS
+    assert within(err, TOL_F16_ABS, "vs oracle")
 
 
 def test_config5_verify(gpu):
@@ -167,7 +167,7 @@ def test_config5_verify(gpu):
     ref = oracle_out(orc, cfg, cfg["seqs"][0])
     err = abs_err(out, ref)
     print(f"config 5 verify: max abs err {err:.2e}")
-    assert err <= TOL_F16_ABS
+    assert within(err, TOL_F16_ABS, "vs oracle")
 
 
 def test_config5_verify_equals_tokens(gpu):
@@ -201,7 +201,7 @@ def test_f32_cache_equals_int8_unit_scales(gpu):
         (out,) = run_cfg(cfg, gpu)
         err = abs_err(out, ref)
         print(f"kv {kv}: |gpu - reference int8| = {err:.2e}")
-        assert err <= TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+        assert within(err, TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max())), "vs oracle")
 
 
 @pytest.mark.parametrize("hd", [72, 200])
@@ -228,7 +228,7 @@ def test_int8_rows_of_8_mod_16_bytes(hd, gpu):
         torch.cuda.synchronize()
     err = abs_err(d["out"].cpu().numpy(), ref)
     print(f"int8 hd {hd}: max abs err {err:.2e}")
-    assert err <= TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+    assert within(err, TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max())), "vs oracle")
 
 
 def block_case(kv, n_kv=8, h=32, hd=128, L=4096, n=64, seed=8100):
@@ -301,7 +301,7 @@ def test_large_block_equals_tokens(kv, gpu):
     bar = TOL_F16_ABS if kv == KV_F16 else TOL_FLOAT_ABS * max(
         1.0, float(np.abs(ref).max()))
     print(f"kv {kv}: large block max abs err {err:.2e} (bar {bar:.1e})")
-    assert err <= bar
+    assert within(err, bar, "vs oracle")
 
 
 def test_large_block_window_and_last(gpu):
@@ -320,7 +320,7 @@ def test_large_block_window_and_last(gpu):
                   last=last, threads=16)
     err = abs_err(blk, ref)
     print(f"large block, window + last: max abs err {err:.2e}")
-    assert err <= TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+    assert within(err, TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max())), "vs oracle")
 
 
 def test_large_block_ragged_sequences(gpu):
