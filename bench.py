@@ -208,7 +208,8 @@ def cpu_prefill_baseline(w, block=64, every=8):
 NCOPY = 6  # 6 caches of 67 MB: more than the 256 MB infinity cache
 
 
-def bench_decode(torch, jm, w, steps, warmup, kv=None, ncopy=NCOPY):
+def bench_decode(torch, jm, w, steps, warmup, kv=None, ncopy=NCOPY,
+                 scores=None):
     """Decode steps (split + merge kernels) launched back to back on one
     stream, each over the next of ncopy copies of the cache - a real decode
     reads another layer's cache each call, so none stays in the 256 MB
@@ -225,7 +226,8 @@ def bench_decode(torch, jm, w, steps, warmup, kv=None, ncopy=NCOPY):
     q = torch.from_numpy(w["q"]).to(dev)
     g = torch.from_numpy(w["g"]).to(dev) if "g" in w else None
     out = torch.empty_like(q)
-    a = jm.Attention(w["h"], w["kvh"], w["hd"], w["L"])
+    a = jm.Attention(w["h"], w["kvh"], w["hd"], w["L"], 1,
+                     jm.FLOAT if scores is None else scores)
     a.set_scale(w["scale"])
     # a stream of its own: the legacy default stream's handle is 0, which
     # the library reads as "the instance's stream" - the events must be on
@@ -454,17 +456,24 @@ def wide_leg(torch, jm, steps, warmup):
 def int_decode_leg(torch, jm, steps, warmup):
     """Config 4's decode over int8 and int16 caches: the step (split +
     merge), with the split kernel's own time and HBM rate. Bytes: keys,
-    values and their scales once."""
+    values and their scales once. int8 twice: the FLOAT scores way, and the
+    INT16 way (which AUTO resolves to at this context, as the
+    reference's)."""
     res = {}
-    for name, dtype, kv, ncopy in (("4-int8", np.int8, jm.KV_I8, 8),
-                                   ("4-int16", np.int16, jm.KV_I16, 5)):
+    for name, dtype, kv, ncopy, scores in (
+            ("4-int8", np.int8, jm.KV_I8, 8, jm.FLOAT),
+            ("4-int8-int16", np.int8, jm.KV_I8, 8, jm.INT16),
+            ("4-int16", np.int16, jm.KV_I16, 5, jm.FLOAT)):
         w = int_decode_workload(dtype)
         ms, _, split_ms, merge_ms = bench_decode(torch, jm, w, steps, warmup,
-                                                 kv=kv, ncopy=ncopy)
+                                                 kv=kv, ncopy=ncopy,
+                                                 scores=scores)
         b = 2 * w["k"].nbytes + 2 * w["ks"].nbytes
+        way = "INT16" if scores == jm.INT16 else "FLOAT"
         res[name] = {"workload": "decode, 16 Q / 2 KV heads, head_dim 256, "
                                  f"32768 positions, {np.dtype(dtype).name} "
-                                 "K/V with per-row scales, f32 q, gated",
+                                 "K/V with per-row scales, f32 q, gated, "
+                                 f"{way} scores",
                      "ms": round(ms, 5), "value": round(b / (ms * 1e-3) / 1e9, 1),
                      "unit": "GB/s", "kv_bytes": b, "bound": "hbm",
                      "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -1,3 +1,8 @@
+/* SPDX-License-Identifier: GPL-3.0-or-later
+ * Restates, nearly line for line where bit-exactness needs it, code of
+ * Janas-LLM, Copyright (C) 2026 Maurizio Cammalleri, GPL-3.0-or-later:
+ * att_weights_ref, janas_exp_det, quant_worker, att_wquant_ref and
+ * the item / merge steps of src/llm/attention.c and src/llm/vmath.h. */
 /*
  * attn_oracle.c - CPU restatement of Janas-LLM's KV-cache attention.
  *

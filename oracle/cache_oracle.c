@@ -1,3 +1,9 @@
+/* SPDX-License-Identifier: GPL-3.0-or-later
+ * Restates, nearly line for line where bit-exactness needs it, code of
+ * Janas-LLM, Copyright (C) 2026 Maurizio Cammalleri, GPL-3.0-or-later:
+ * q8_32_ref, janas_q8k_quantize (src/llm/quant.c), rms_norm,
+ * rope_neox and the key / value part of qkv_item (src/llm/model_impl.h,
+ * src/llm/model_attn.c) and the shift rules of src/llm/model.c. */
 /*
  * cache_oracle.c - CPU restatement of the cache-side rules (see
  * cache_oracle.h). TEST INFRASTRUCTURE ONLY. Each function follows the

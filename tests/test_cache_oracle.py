@@ -273,3 +273,58 @@ def test_rotate_then_unrotate_is_identity_within_quanta():
     z1 = orc.unrotate_row(fwd, z, cs[0], -sn[0])
     z2 = orc.unrotate_row(fwd, z1, cs[0], sn[0])
     assert np.abs(fwd * np.float64(z2) - row * np.float64(z)).max() <= 2 * z2
+
+
+def q_prep_ok(q, got, w, cs, sn, n_rot, eps, tol=2e-6):
+    """orc_q_prep against its closed form in float64: each (token, head)
+    row rms-normalized with weights w (model_attn.c:93-94), then rotated in
+    pairs (i, i + n_rot / 2) by the token's angles (model_attn.c:95-96,
+    model_impl.h:635-644); within tol of the largest magnitude."""
+    n, n_head, hd = q.shape
+    half = n_rot // 2
+    for j in range(n):
+        for h in range(n_head):
+            x = q[j, h].astype(np.float64)
+            if w is not None:
+                x = x / np.sqrt((x * x).mean() + eps) * w
+            a, b = x[:half].copy(), x[half:n_rot].copy()
+            x[:half] = a * cs[j] - b * sn[j]
+            x[half:n_rot] = a * sn[j] + b * cs[j]
+            if np.abs(got[j, h] - x).max() > tol * max(1.0, np.abs(x).max()):
+                return False
+    return True
+
+
+def test_q_prep_against_float64_and_planted_mistakes():
+    """The query side of qkv_item: norm, then rotation; the bound is a few
+    float roundings. Planted mistakes - the rotation turned the other way,
+    the norm's weights dropped, pairs (2i, 2i + 1) - are caught."""
+    n, n_head, hd, n_rot, eps = 3, 4, 128, 96, 1e-6
+    q = (2.0 * RNG.standard_normal((n, n_head, hd))).astype(np.float32)
+    w = RNG.uniform(0.5, 1.5, hd).astype(np.float32)
+    cs, sn = rope_tables(range(40, 40 + n), n_rot)
+
+    def prep(x, **kw):
+        x = np.ascontiguousarray(x.copy())
+        orc.q_prep(x, **kw)
+        return x
+
+    got = prep(q, cs=cs, sn=sn, n_rot=n_rot, q_norm=w, eps=eps)
+    assert q_prep_ok(q, got, w, cs, sn, n_rot, eps)
+    # no norm: the rotation alone, and columns past n_rot untouched
+    got = prep(q, cs=cs, sn=sn, n_rot=n_rot)
+    assert q_prep_ok(q, got, None, cs, sn, n_rot, eps)
+    assert np.array_equal(got[:, :, n_rot:], q[:, :, n_rot:])
+    # planted mistakes
+    bad = prep(q, cs=cs, sn=-sn, n_rot=n_rot, q_norm=w, eps=eps)
+    assert not q_prep_ok(q, bad, w, cs, sn, n_rot, eps)
+    bad = prep(q, cs=cs, sn=sn, n_rot=n_rot, q_norm=np.ones(hd, np.float32),
+               eps=eps)
+    assert not q_prep_ok(q, bad, w, cs, sn, n_rot, eps)
+    perm = np.arange(hd)
+    perm[:n_rot] = np.concatenate([np.arange(0, n_rot, 2),
+                                   np.arange(1, n_rot, 2)])
+    bad = prep(q[:, :, perm], cs=cs, sn=sn, n_rot=n_rot)
+    unperm = np.empty_like(bad)
+    unperm[:, :, perm] = bad
+    assert not q_prep_ok(q, unperm, None, cs, sn, n_rot, eps)
