@@ -140,11 +140,14 @@ int describe(const janas_attn *a, int kv, const janas_attn_seq &s, SeqDesc &d)
     d.rtiles = (s.n * a->group + tr - 1) / tr;
     if (s.out_q8k && ((uint64_t)a->n_head * a->hd) % JANAS_ATTN_QK)
         return JANAS_ATTN_EINVAL;
+    d.q8k = s.out_q8k;
     return JANAS_ATTN_OK;
 }
 
 /* The outputs also as Q8_K blocks where a sequence asks for them
-   (att_out_tok, model_attn.c:159-170: the gate is already in the output). */
+   (att_out_tok, model_attn.c:159-170: the gate is already in the output):
+   the prefill path's pass over its outputs (the split path's merge
+   quantizes its own). */
 int put_q8k(const janas_attn *a, const janas_attn_seq *seqs, uint32_t n_seqs,
             hipStream_t stream)
 {
@@ -304,12 +307,19 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
         SplitArgs args;
         memset(&args, 0, sizeof args);
         uint64_t rows = 0, pairs = 0;
-        for (uint32_t i = 0; i < m; i++)
+        bool q8k = false;
+        for (uint32_t i = 0; i < m; i++) {
             pairs += (uint64_t)seqs[s0 + i].n * a->n_head;
-        args.merge_cols = merge_cols(pairs, a->hd);
+            q8k |= seqs[s0 + i].out_q8k != nullptr;
+        }
+        /* a sequence that asks for Q8_K blocks: the merge takes a block a
+           workgroup and quantizes it (the same output bits) */
+        args.merge_cols = q8k ? kMergeQ8k : merge_cols(pairs, a->hd);
         args.once = 1;
         uint32_t wg = 0, mg = 0;
+        /* merge workgroups a (token, head), or a token's blocks */
         const uint32_t nd = (a->hd + args.merge_cols - 1) / args.merge_cols;
+        const uint32_t nb = (uint32_t)((uint64_t)a->n_head * a->hd / JANAS_ATTN_QK);
         for (uint32_t i = 0; i < m; i++) {
             SeqDesc &d = args.seq[i];
             int rc = describe(a, kv, seqs[s0 + i], d);
@@ -320,7 +330,7 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
             d.part0 = rows;
             args.once &= d.rtiles == 1;
             uint64_t nwg = (uint64_t)a->n_kv * d.span * d.rtiles;
-            uint64_t nmg = (uint64_t)d.n * a->n_head * nd;
+            uint64_t nmg = q8k ? (uint64_t)d.n * nb : (uint64_t)d.n * a->n_head * nd;
             if (wg + nwg > 0x7FFFFFFFu || mg + nmg > 0x7FFFFFFFu)
                 return JANAS_ATTN_ERANGE;
             wg += (uint32_t)nwg;
@@ -434,6 +444,9 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
         prof_end(ev, stream);
         if (e != hipSuccess)
             return hip_err(e, "prefill launch");
+        int rc = put_q8k(a, seqs + s0, m, stream);
+        if (rc)
+            return rc;
     }
     return JANAS_ATTN_OK;
 }
@@ -844,7 +857,7 @@ extern "C" int janas_attn_run_dev_split(struct janas_attn *a, int kv_type,
         return rc;
     hipStream_t st = stream ? (hipStream_t)stream : a->stream;
     rc = run_split(a, kv_type, gate_mode, seqs, n_seqs, st);
-    return note(a, rc ? rc : put_q8k(a, seqs, n_seqs, st));
+    return note(a, rc);
 }
 
 extern "C" int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
@@ -857,7 +870,7 @@ extern "C" int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
         return rc;
     hipStream_t st = stream ? (hipStream_t)stream : a->stream;
     rc = run_prefill(a, kv_type, gate_mode, seqs, n_seqs, st);
-    return note(a, rc ? rc : put_q8k(a, seqs, n_seqs, st));
+    return note(a, rc);
 }
 
 namespace {
@@ -907,7 +920,7 @@ int run_dev(janas_attn *a, int kv_type, int gate_mode, const janas_attn_seq *seq
     } else {
         rc = run_split(a, kv_type, gate_mode, seqs, n_seqs, st, 3, fixed);
     }
-    return note(a, rc ? rc : put_q8k(a, seqs, n_seqs, st));
+    return note(a, rc);
 }
 
 }  // namespace

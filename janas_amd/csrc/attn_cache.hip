@@ -33,6 +33,7 @@
 #include <hip/hip_runtime.h>
 
 #include "attn_kernels.h"
+#include "attn_q8k.h"
 
 namespace janas {
 namespace {
@@ -222,57 +223,9 @@ __global__ __launch_bounds__(64 * kRowWaves) void shift_kernel(const ShiftArgs A
  */
 __global__ __launch_bounds__(256) void q8k_kernel(const Q8kArgs A)
 {
-    __shared__ float sRed[8];
-    __shared__ int sSum[16];
-    __shared__ __attribute__((aligned(16))) uint8_t sBlk[kQ8kBytes];
+    __shared__ Q8kLds S;
     const uint32_t t = threadIdx.x, b = blockIdx.x;
-    const uint32_t w = t >> 6, lane = t & 63;
-    const float x = A.x[(size_t)b * 256 + t];
-    /* the 256's largest magnitude (waves, then across) and the 32's */
-    float m = wave_max(fabsf(x));
-    float m32 = fabsf(x);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1)
-        m32 = fmaxf(m32, __shfl_xor(m32, o, 64));
-    if (lane == 0)
-        sRed[w] = m;
-    __syncthreads();
-    const float amax = fmaxf(fmaxf(sRed[0], sRed[1]), fmaxf(sRed[2], sRed[3]));
-    const float d = amax / 127.0f;
-    const float id = d > 0.0f ? 1.0f / d : 0.0f;
-    float q = rintf(x * id);
-    q = q > 127.0f ? 127.0f : q < -127.0f ? -127.0f : q;
-    const float d32 = m32 / 127.0f;
-    const float id32 = d32 > 0.0f ? 1.0f / d32 : 0.0f;
-    float q32 = rintf(x * id32);
-    q32 = q32 > 127.0f ? 127.0f : q32 < -127.0f ? -127.0f : q32;
-    /* block layout: d @0, qs @4, bsums @260, d32 @292, qs32 @324,
-       bsums32 @580, bsums2 @612 (struct janas_block_q8k, quant.h:283-300) */
-    sBlk[4 + t] = (uint8_t)(int8_t)q;
-    sBlk[324 + t] = (uint8_t)(int8_t)q32;
-    if (t == 0)
-        *(float *)&sBlk[0] = d;
-    if ((t & 31) == 0)
-        *(float *)&sBlk[292 + 4 * (t / 32)] = d32;
-    /* sums of 16: integers, exact in any order */
-    int s = (int)q, s32 = (int)q32;
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) {
-        s += __shfl_xor(s, o, 64);
-        s32 += __shfl_xor(s32, o, 64);
-    }
-    if ((t & 15) == 0) {
-        *(int16_t *)&sBlk[260 + 2 * (t / 16)] = (int16_t)s;
-        *(int16_t *)&sBlk[580 + 2 * (t / 16)] = (int16_t)s32;
-        sSum[t / 16] = s;
-    }
-    __syncthreads();
-    if (t < 8)
-        *(int16_t *)&sBlk[612 + 2 * t] = (int16_t)(sSum[2 * t] + sSum[2 * t + 1]);
-    __syncthreads();
-    uint8_t *dst = A.y + (size_t)b * kQ8kBytes;
-    if (t < kQ8kBytes / 4)
-        *(uint32_t *)(dst + 4 * t) = *(const uint32_t *)&sBlk[4 * t];
+    q8k_block(A.x[(size_t)b * 256 + t], t, A.y + (size_t)b * kQ8kBytes, S);
 }
 
 }  // namespace

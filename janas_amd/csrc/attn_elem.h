@@ -83,15 +83,25 @@ template <> struct Elem<kI8> {
     {
         return Raw{*(const uint2 *)((const int8_t *)b + i)};
     }
+    /* 4 signed bytes to 4 halves, exactly: byte b ^ 0x80 = b + 128 as the
+       low mantissa byte under the high byte 0x64 is the half 1024 + b +
+       128 (halves in [1024, 2048) step by 1), less 1152 is b - one xor,
+       two byte permutes and two packed adds for 4 numbers */
+    __device__ static void widen4(uint32_t x, h2 &a, h2 &b)
+    {
+        const uint32_t u = x ^ 0x80808080u;
+        const uint32_t pa = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+        const uint32_t pb = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+        const h2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+        a = __builtin_bit_cast(h2, pa) - off;
+        b = __builtin_bit_cast(h2, pb) - off;
+    }
     __device__ static h8 widen(uint32_t lo, uint32_t hi)
     {
-        h8 r;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            r[e] = (_Float16)(int)(int8_t)(lo >> (8 * e));
-            r[4 + e] = (_Float16)(int)(int8_t)(hi >> (8 * e));
-        }
-        return r;
+        h2 p[4];
+        widen4(lo, p[0], p[1]);
+        widen4(hi, p[2], p[3]);
+        return h8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
     }
     __device__ static void planes8(const Raw &r, h8 *p)
     {

@@ -21,6 +21,8 @@ constexpr uint32_t kChunk = 256;
 constexpr uint32_t kTileRows = 8;
 constexpr uint32_t kWideRows = 16;
 inline uint32_t split_tile_rows(uint32_t hd) { return hd > 256 ? kWideRows : kTileRows; }
+/* merge_cols of a merge that also puts its outputs into Q8_K blocks */
+constexpr uint32_t kMergeQ8k = 256;
 /* sequences one launch takes (by value in its arguments) */
 constexpr uint32_t kMaxSeqs = 16;
 /* merge workgroups a launch keeps at least when it takes 128 columns a
@@ -48,6 +50,7 @@ struct SeqDesc {
     uint32_t nseg;         /* prefill: key segments a row block is split
                               into (1: none, the output is written directly) */
     uint64_t part0;        /* first partial row (of m, l and hd values) */
+    void *q8k;             /* the output also as Q8_K blocks, or null */
 };
 
 struct SplitArgs {
@@ -56,7 +59,8 @@ struct SplitArgs {
     float *part_acc;       /* [rows][hd]: weighted values */
     uint32_t n_seqs, n_wg;
     uint32_t once;         /* every sequence one row tile: K/V read once */
-    uint32_t merge_cols;   /* 32 or 128 columns a merge workgroup */
+    uint32_t merge_cols;   /* 32 or 128 columns a merge workgroup, or
+                              kMergeQ8k: one Q8_K block of 256 outputs */
     uint32_t n_head, n_kv, group, hd, window;
     float scale;
     int ring;

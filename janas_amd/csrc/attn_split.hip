@@ -45,6 +45,7 @@
 #include <hip/hip_runtime.h>
 
 #include "attn_elem.h"
+#include "attn_q8k.h"
 
 namespace janas {
 namespace {
@@ -105,6 +106,9 @@ template <int T, int D> struct SS {
     static constexpr int NT = D / 16;                /* value column tiles */
     static constexpr int DP = Elem<T>::planes;       /* data planes a product */
     static constexpr bool SCALED = T == kI8 || T == kI16;
+    /* groups in flight a wave (deeper measured no faster: int8 rows
+       with 4 in flight took 8% longer at config 4's shape) */
+    static constexpr int NF = 2;
     static_assert(LG >= 1 && kSG * MRB % 1024 == 0, "whole kilobytes a group");
     static_assert(REG >= 32 * D, "the region holds the wave's sums");
 };
@@ -244,9 +248,17 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
             vr[s][l] = NT ? __builtin_nontemporal_load((const u4 *)(vbase + addr(s, l)))
                           : *(const u4 *)(vbase + addr(s, l));
     };
-    kload(0);
+    /* group i of the wave's 8: K groups 0..3, then V groups 0..3 */
+    auto issue = [&](int i) {
+        if (i < kSNG)
+            kload(i);
+        else if (i < 2 * kSNG)
+            vload(i - kSNG);
+    };
+    constexpr int NF = S::NF;
+    issue(0);
     __builtin_amdgcn_sched_barrier(0);
-    kload(1);
+    issue(1);
     __builtin_amdgcn_sched_barrier(0);
 
     /* ---- the query planes: scaled by 2^e so that the row's largest |q|
@@ -300,6 +312,12 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
         sVs[w][lane] = vsv;
     }
     __builtin_amdgcn_sched_barrier(0);
+    /* the rest of the groups in flight, now that the query is in */
+#pragma unroll
+    for (int i = 2; i < NF; i++) {
+        issue(i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     __syncthreads();
     h8 qb[KS];
 #pragma unroll
@@ -349,10 +367,7 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
             for (int l = 0; l < LG; l++)
                 t[l] = kr[s][l];
             __builtin_amdgcn_sched_barrier(0);
-            if (s + 2 < kSNG)
-                kload(s + 2);
-            else
-                vload(s + 2 - kSNG);
+            issue(s + NF);
             __builtin_amdgcn_sched_barrier(0);
             if (s > 0)
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -496,8 +511,7 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
             for (int l = 0; l < LG; l++)
                 t[l] = vr[s][l];
             __builtin_amdgcn_sched_barrier(0);
-            if (s + 2 < kSNG)
-                vload(s + 2);
+            issue(kSNG + s + NF);
             __builtin_amdgcn_sched_barrier(0);
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
@@ -632,13 +646,21 @@ __global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
 
 /*
  * Merge of the chunk partials of (token j, query head h), 32 or 128 columns
- * a workgroup (attention.c:870-910). Group g of 8 (32 lanes each, a lane a
- * column) takes chunks g, g + 8, ... of the token's range, 16 at a time in
- * one batch of loads: their largest score M_g, then sum_c e^(m_c - M_g) l_c
- * and acc_c in chunk order. The groups are combined with weights
- * e^(M_g - M) as ((g0 + g1) + (g2 + g3)) + ((g4 + g5) + (g6 + g7)). The
- * order depends only on the token's own chunk range, so a token merges the
- * same way in any block. The gate sigmoid(g) * o is applied on the way out.
+ * a workgroup (attention.c:870-910). Group g of 8 (32 lanes each, a lane
+ * CPL columns) takes chunks g, g + 8, ... of the token's range, 16 at a
+ * time in one batch of loads: their largest score M_g, then
+ * sum_c e^(m_c - M_g) l_c and acc_c in chunk order. The groups are combined
+ * with weights e^(M_g - M) as ((g0 + g1) + (g2 + g3)) + ((g4 + g5) +
+ * (g6 + g7)). The order depends only on the token's own chunk range, so a
+ * token merges the same way in any block. The gate sigmoid(g) * o is
+ * applied on the way out.
+ *
+ * Q8K: a workgroup takes one block of 256 of the token's n_head x hd
+ * outputs instead (a lane 8 consecutive ones, of one head since hd is a
+ * multiple of 8), merges them with the same arithmetic column by column -
+ * so the outputs are the same bits - and quantizes them into the block's
+ * Q8_K (attn_merge.comp:78-138 does the same in the reference's GPU path):
+ * no pass of its own for the quantization.
  */
 constexpr int kMergeGroups = 8;
 constexpr int kMergeLanes = 32;            /* lanes a group */
@@ -651,27 +673,50 @@ __device__ __forceinline__ float &f4e(float4 &v, int e)
 }
 
 /*
- * CPL columns a lane (1 or 4: 32 or 128 columns a workgroup). Each column's
- * arithmetic is the same in both, so a token's output does not depend on
- * the instance its call takes; 4 when a launch has (token, head) pairs
- * enough to fill the GPU with 4 times fewer workgroups (blocks of tokens),
- * 1 when it has few (a decode spreads its loads over more CUs).
+ * CPL columns a lane (1, 4 or 8: 32, 128 or 256 columns a workgroup). Each
+ * column's arithmetic is the same in all, so a token's output does not
+ * depend on the instance its call takes; 4 when a launch has (token, head)
+ * pairs enough to fill the GPU with 4 times fewer workgroups (blocks of
+ * tokens), 1 when it has few (a decode spreads its loads over more CUs), 8
+ * with Q8K.
  */
-template <int CPL, bool ONE = false>
+template <int CPL, bool ONE = false, bool Q8K = false>
 __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 {
+    static_assert(CPL == 1 || CPL == 4 || CPL == 8, "1, 4 or 8 columns a lane");
+    static_assert(!Q8K || CPL == 8, "a Q8_K block: 256 columns");
+    constexpr int NV = CPL >= 4 ? CPL / 4 : 1;  /* float4s a lane */
     constexpr uint32_t kCols = kMergeLanes * CPL;
-    __shared__ float sM[kMergeGroups], sL[kMergeGroups];
-    __shared__ float4 sAcc[kMergeGroups][kMergeLanes];
+    /* a lane's own largest score and sum (with Q8K the lanes of a
+       workgroup may belong to different heads) */
+    __shared__ float sM[kMergeGroups][kMergeLanes], sL[kMergeGroups][kMergeLanes];
+    __shared__ float4 sAcc[kMergeGroups][NV][kMergeLanes];
+    __shared__ float sOut[Q8K ? 256 : 1];
+    __shared__ Q8kLds sQ;
     const uint32_t id = blockIdx.x, tid = threadIdx.x;
     const uint32_t g = tid / kMergeLanes, cl = tid % kMergeLanes;
     uint32_t si = 0;
     if constexpr (!ONE)
         si = seq_index(A, &SeqDesc::mg0, id);
     const SeqDesc &sq = A.seq[si];
-    const uint32_t hd = A.hd, G = A.group, nd = (hd + kCols - 1) / kCols;
-    const uint32_t local = id - sq.mg0, db = local % nd;
-    const uint32_t h = (local / nd) % A.n_head, j = local / nd / A.n_head;
+    const uint32_t hd = A.hd, G = A.group;
+    const uint32_t local = id - sq.mg0;
+    /* the lane's token j, head h and columns col .. col + CPL - 1 (hd is a
+       multiple of 8: all are inside the row or none is) */
+    uint32_t j, h, col, blk = 0;
+    if constexpr (Q8K) {
+        const uint32_t nb = A.n_head * hd / 256;   /* blocks a token */
+        j = local / nb;
+        blk = local % nb;
+        const uint32_t e0 = 256 * blk + CPL * cl;
+        h = e0 / hd;
+        col = e0 % hd;
+    } else {
+        const uint32_t nd = (hd + kCols - 1) / kCols, db = local % nd;
+        h = (local / nd) % A.n_head;
+        j = local / nd / A.n_head;
+        col = db * kCols + CPL * cl;
+    }
     const uint32_t kvh = h / G, r = j * G + h % G, R = sq.n * G;
     const uint32_t pos = sq.pos0 + j;
     /* last[] past the call's end would read partials of other rows */
@@ -681,9 +726,6 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     const uint32_t clo = lo / kChunk, nc = hi / kChunk - clo + 1;
     /* partial row of chunk clo + i */
     const uint64_t base = sq.part0 + ((uint64_t)kvh * sq.span + (clo - sq.c0)) * R + r;
-    /* the lane's columns col .. col + CPL - 1 (hd is a multiple of 8: all
-       are inside the row or none is) */
-    const uint32_t col = db * kCols + CPL * cl;
     const bool colok = col < hd;
     /* the gate, asked for with the partials so the loads overlap: branch-
        free (a load under a branch is waited for where the branches join,
@@ -693,17 +735,26 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     const float *gsrc = gel ? sq.gate + oi : A.part_ml;
     const float *hsrc = A.gate_mode == kGateHead ? sq.gate + (size_t)j * A.n_head + h
                                                  : A.part_ml;
-    float4 gv = {0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (CPL == 4)
-        gv = *(const float4 *)gsrc;
-    else
-        gv.x = *gsrc;
+    float4 gv[NV];
+#pragma unroll
+    for (int u = 0; u < NV; u++)
+        gv[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (CPL >= 4) {
+#pragma unroll
+        for (int u = 0; u < NV; u++)
+            gv[u] = ((const float4 *)gsrc)[gel ? u : 0];
+    } else {
+        gv[0].x = *gsrc;
+    }
     const float gh = *hsrc;
     float mg = -INFINITY, lg = 0.0f;
-    float4 ag = {0.0f, 0.0f, 0.0f, 0.0f};
+    float4 ag[NV];
+#pragma unroll
+    for (int u = 0; u < NV; u++)
+        ag[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
     for (uint32_t i0 = g; i0 < nc; i0 += kMergeGroups * kMergeBatch) {
         float2 ml[kMergeBatch];
-        float4 v[kMergeBatch];
+        float4 v[kMergeBatch][NV];
         /* branch-free: chunks past the range read the last one, weight 0 */
 #pragma unroll
         for (int b = 0; b < kMergeBatch; b++) {
@@ -711,10 +762,13 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
             const uint64_t pr = base + (uint64_t)i * R;
             ml[b] = *(const float2 *)(A.part_ml + pr * 2);
             const float *src = A.part_acc + pr * hd + (colok ? col : 0);
-            if constexpr (CPL == 4)
-                v[b] = *(const float4 *)src;
-            else
-                v[b].x = *src;
+            if constexpr (CPL >= 4) {
+#pragma unroll
+                for (int u = 0; u < NV; u++)
+                    v[b][u] = ((const float4 *)src)[u];
+            } else {
+                v[b][0].x = *src;
+            }
         }
         float mb = mg;
 #pragma unroll
@@ -727,60 +781,71 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
         lg *= f;
 #pragma unroll
         for (int e = 0; e < CPL; e++)
-            f4e(ag, e) *= f;
+            f4e(ag[e / 4], e % 4) *= f;
 #pragma unroll
         for (int b = 0; b < kMergeBatch; b++) {
             const float wgt = i0 + kMergeGroups * b < nc ? __builtin_amdgcn_exp2f(ml[b].x - mb) : 0.0f;
             lg += wgt * ml[b].y;
 #pragma unroll
             for (int e = 0; e < CPL; e++)
-                f4e(ag, e) = fmaf(wgt, f4e(v[b], e), f4e(ag, e));
+                f4e(ag[e / 4], e % 4) = fmaf(wgt, f4e(v[b][e / 4], e % 4), f4e(ag[e / 4], e % 4));
         }
         mg = mb;
     }
-    if (cl == 0) {
-        sM[g] = mg;
-        sL[g] = lg;
-    }
-    sAcc[g][cl] = ag;
+    sM[g][cl] = mg;
+    sL[g][cl] = lg;
+#pragma unroll
+    for (int u = 0; u < NV; u++)
+        sAcc[g][u][cl] = ag[u];
     __syncthreads();
-    if (g != 0 || !colok)
-        return;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < kMergeGroups; k++)
-        mx = fmaxf(mx, sM[k]);
-    float wl[kMergeGroups];
-    float4 wa[kMergeGroups];
-#pragma unroll
-    for (int k = 0; k < kMergeGroups; k++) {
-        const float wk = sM[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sM[k] - mx);
-        float4 a = sAcc[k][cl];
-        wl[k] = wk * sL[k];
-#pragma unroll
-        for (int e = 0; e < CPL; e++)
-            f4e(wa[k], e) = wk * f4e(a, e);
-    }
-    const float sum = ((wl[0] + wl[1]) + (wl[2] + wl[3])) + ((wl[4] + wl[5]) + (wl[6] + wl[7]));
-    const float inv = 1.0f / sum;
-    float4 o;
-#pragma unroll
-    for (int e = 0; e < CPL; e++) {
-        float x[kMergeGroups];
+    if (g == 0 && colok) {
+        float mx = -INFINITY;
 #pragma unroll
         for (int k = 0; k < kMergeGroups; k++)
-            x[k] = f4e(wa[k], e);
-        float y = (((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]))) * inv;
-        if (A.gate_mode == kGateElem)
-            y *= 1.0f / (1.0f + expf(-f4e(gv, e)));
-        else if (A.gate_mode == kGateHead)
-            y *= 1.0f / (1.0f + expf(-gh));
-        f4e(o, e) = y;
+            mx = fmaxf(mx, sM[k][cl]);
+        float wl[kMergeGroups], wk[kMergeGroups];
+#pragma unroll
+        for (int k = 0; k < kMergeGroups; k++) {
+            wk[k] = sM[k][cl] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sM[k][cl] - mx);
+            wl[k] = wk[k] * sL[k][cl];
+        }
+        const float sum = ((wl[0] + wl[1]) + (wl[2] + wl[3])) + ((wl[4] + wl[5]) + (wl[6] + wl[7]));
+        const float inv = 1.0f / sum;
+        float4 o[NV];
+#pragma unroll
+        for (int e = 0; e < CPL; e++) {
+            float x[kMergeGroups];
+#pragma unroll
+            for (int k = 0; k < kMergeGroups; k++) {
+                float4 a = sAcc[k][e / 4][cl];
+                x[k] = wk[k] * f4e(a, e % 4);
+            }
+            float y = (((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]))) * inv;
+            if (A.gate_mode == kGateElem)
+                y *= 1.0f / (1.0f + expf(-f4e(gv[e / 4], e % 4)));
+            else if (A.gate_mode == kGateHead)
+                y *= 1.0f / (1.0f + expf(-gh));
+            f4e(o[e / 4], e % 4) = y;
+            if constexpr (Q8K)
+                sOut[CPL * cl + e] = y;
+        }
+        if constexpr (CPL >= 4) {
+#pragma unroll
+            for (int u = 0; u < NV; u++)
+                ((float4 *)(sq.out + oi))[u] = o[u];
+        } else {
+            sq.out[oi] = o[0].x;
+        }
     }
-    if constexpr (CPL == 4)
-        *(float4 *)(sq.out + oi) = o;
-    else
-        sq.out[oi] = o.x;
+    if constexpr (Q8K) {
+        /* every thread: the block's number tid, quantized (the same bits
+           as the Q8_K pass over the output) */
+        if (sq.q8k == nullptr)
+            return;  /* a sequence of the launch that asked for none */
+        __syncthreads();
+        const uint32_t nb = A.n_head * hd / 256;
+        q8k_block(sOut[tid], tid, (uint8_t *)sq.q8k + ((size_t)j * nb + blk) * kQ8kBytes, sQ);
+    }
 }
 
 template <int T, int D>
@@ -856,7 +921,11 @@ uint32_t merge_cols(uint64_t pairs, uint32_t hd)
 hipError_t launch_merge(const SplitArgs &a, uint32_t n_wg, hipStream_t s)
 {
     const bool one = a.n_seqs == 1;
-    if (a.merge_cols == 128 && one)
+    if (a.merge_cols == kMergeQ8k && one)
+        hipLaunchKernelGGL((merge_kernel<8, true, true>), dim3(n_wg), dim3(256), 0, s, a);
+    else if (a.merge_cols == kMergeQ8k)
+        hipLaunchKernelGGL((merge_kernel<8, false, true>), dim3(n_wg), dim3(256), 0, s, a);
+    else if (a.merge_cols == 128 && one)
         hipLaunchKernelGGL((merge_kernel<4, true>), dim3(n_wg), dim3(256), 0, s, a);
     else if (a.merge_cols == 128)
         hipLaunchKernelGGL(merge_kernel<4>, dim3(n_wg), dim3(256), 0, s, a);

@@ -247,6 +247,50 @@ def test_q8k_output_bitwise(gpu, path, gate_mode):
     assert within(abs_err(o, ref), TOL_F16_ABS, "abs_err(o, ref)")
 
 
+@pytest.mark.parametrize("geom", [(32, 8, 128, 1), (8, 2, 96, 3),
+                                  (16, 2, 256, 1), (16, 4, 64, 5),
+                                  (4, 1, 512, 2)])
+@pytest.mark.parametrize("gate_mode", [jm.GATE_NONE, jm.GATE_HEAD])
+def test_q8k_fused_merge(gpu, geom, gate_mode):
+    """The split path's merge quantizes its own output, a Q8_K block a
+    workgroup (blocks across heads for head sizes 64, 96 and 128, half a
+    head at 512): the blocks equal the restatement of janas_q8k_quantize
+    over the output bit for bit, and the output equals the same call's
+    without Q8_K bit for bit (a second sequence of the launch asks for
+    none)."""
+    h, kvh, hd, n = geom
+    L = 900
+    rng = np.random.default_rng(hd + n)
+    k = rng.standard_normal((kvh, L, hd)).astype(np.float16)
+    v = rng.standard_normal((kvh, L, hd)).astype(np.float16)
+    q = rng.standard_normal((n, h, hd)).astype(np.float32)
+    g = rng.standard_normal((n, h)).astype(np.float32)
+    kd, vd, qd, gd = dev(k, gpu), dev(v, gpu), dev(q, gpu), dev(g, gpu)
+    nb = h * hd // 256
+    outs = [torch.zeros((n, h, hd), dtype=torch.float32, device=gpu)
+            for _ in range(3)]
+    blocks = torch.zeros((n, nb, jm.attention.Q8K_BYTES), dtype=torch.uint8,
+                         device=gpu)
+    seq = dict(k=kd, v=vd, q=qd, gate=gd, cap=L, n=n, pos0=L - n)
+    with jm.Attention(h, kvh, hd, L) as a:
+        a.run_dev(KV_F16, [dict(seq, out=outs[0], out_q8k=blocks),
+                           dict(seq, out=outs[1])],
+                  gate_mode=gate_mode, path="split")
+        a.run_dev(KV_F16, [dict(seq, out=outs[2])], gate_mode=gate_mode,
+                  path="split")
+        torch.cuda.synchronize()
+    o = [x.cpu().numpy() for x in outs]
+    assert np.array_equal(o[0].view(np.int32), o[2].view(np.int32))
+    assert np.array_equal(o[1].view(np.int32), o[2].view(np.int32))
+    want = orc.q8k_quantize(o[0].reshape(n, h * hd))
+    assert blocks.cpu().numpy().tobytes() == want.tobytes()
+    ref = orc.run(q, k, v, n_head=h, n_kv=kvh, hd=hd, pos0=L - n, kv=KV_F16,
+                  threads=threads())
+    if gate_mode:
+        orc.gate(ref, g, per_head=True)
+    assert within(abs_err(o[0], ref), TOL_F16_ABS, "vs oracle")
+
+
 def test_q8k_output_needs_whole_blocks(gpu):
     h, kvh, hd, L = 3, 1, 64, 256   # 192 numbers a token: no whole block
     k = torch.zeros((kvh, L, hd), dtype=torch.float16, device=gpu)
