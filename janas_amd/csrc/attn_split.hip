@@ -123,12 +123,16 @@ template <int D> __device__ __forceinline__ uint32_t slot(uint32_t u, uint32_t r
 }
 
 /* ONE: a launch of one sequence - its descriptor is read at fixed offsets
-   with the rest of the arguments, not after the launch's sequence count. NT:
+   with the rest of the arguments, not after the launch's sequence count.
+   Head sizes up to 128 over 8- and 16-bit caches ask for 3 waves a SIMD
+   (at most 168 registers): the f16 instance otherwise takes 176 and holds
+   two workgroups a CU, where calls of several row tiles (a verify) or many
+   chunks (a ragged decode) want more in flight. NT:
    every chunk is read by one workgroup (decode): nontemporal loads; the row
    tiles of a block of tokens read a chunk each, and plain loads keep it in
    L2 for them. */
 template <int T, int D, bool NT, bool ONE = false, bool Q16 = false>
-__global__ __launch_bounds__(kSW * 64) void split_kernel(const SplitArgs A)
+__global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 128 && T != kF32 ? 3 : 1))) void split_kernel(const SplitArgs A)
 {
     static_assert(!Q16 || (T == kI8 && D % 16 == 0), "INT16: int8 caches");
     using S = SS<T, D>;
