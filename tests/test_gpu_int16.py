@@ -260,3 +260,48 @@ def test_int16_run_dev_long_prompt_stays_split(gpu):
                   kv=orc.KV_I8, int16=True, threads=threads())
     bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
     assert within(abs_err(auto.cpu().numpy(), ref), bar, "200-token int16")
+
+
+def test_int16_noalloc_and_q8k(gpu):
+    """The INT16 way through run_dev and run_dev_noalloc with the Q8_K
+    output fused into the merge, two sequences a launch: outputs and blocks
+    equal bit for bit, the blocks the restatement's quantization of the
+    output, the output the restatement's INT16 way within the FLOAT bar."""
+    h, kvh, hd, L = 16, 2, 256, 4096
+    k, ks = int8_cache(701, kvh, L, hd)
+    v, vs = int8_cache(702, kvh, L, hd)
+    qs = [normal(703, 3 * h * hd).reshape(3, h, hd),
+          normal(704, 1 * h * hd).reshape(1, h, hd)]
+    pos = [L - 3, 1500]
+    kd, vd, ksd, vsd = (to_dev(x, gpu) for x in (k, v, ks, vs))
+    nb = h * hd // 256
+
+    def seqs(outs, blocks):
+        return [dict(k=kd, v=vd, ks=ksd, vs=vsd, q=to_dev(q, gpu), out=o,
+                     out_q8k=b, cap=L, n=q.shape[0], pos0=p)
+                for q, o, b, p in zip(qs, outs, blocks, pos)]
+
+    res = []
+    with Attention(h, kvh, hd, L, 1, janas_amd.INT16) as a:
+        for path in ("auto", "noalloc"):
+            outs = [torch.full((q.shape[0], h, hd), float("nan"), device=gpu)
+                    for q in qs]
+            blocks = [torch.zeros((q.shape[0], nb, janas_amd.attention.Q8K_BYTES),
+                                  dtype=torch.uint8, device=gpu) for q in qs]
+            a.run_dev(janas_amd.KV_I8, seqs(outs, blocks), path=path)
+            torch.cuda.synchronize()
+            res.append(([o.cpu().numpy() for o in outs],
+                        [b.cpu().numpy() for b in blocks]))
+        assert a.status() == 0
+    (o1, b1), (o2, b2) = res
+    for x, y in zip(o1, o2):
+        assert np.array_equal(x.view(np.int32), y.view(np.int32))
+    for x, y in zip(b1, b2):
+        assert x.tobytes() == y.tobytes()
+    for q, o, b, p in zip(qs, o1, b1, pos):
+        n = q.shape[0]
+        assert b.tobytes() == orc.q8k_quantize(o.reshape(n, h * hd)).tobytes()
+        ref = orc.run(q, k, v, ks, vs, n_head=h, n_kv=kvh, hd=hd, pos0=p,
+                      kv=orc.KV_I8, int16=True, threads=threads())
+        bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+        assert within(abs_err(o, ref), bar, f"int16 noalloc q8k n={n}")
