@@ -367,7 +367,7 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
    give each unit a workgroup, at least kSegTiles key tiles each. It
    depends on the sequence alone, so a sequence's result is the same in
    any launch. */
-constexpr uint32_t kSegTiles = 6, kMaxSeg = 16;
+constexpr uint32_t kSegTiles = 6;
 
 uint32_t prefill_segments(const janas_attn *a, const SeqDesc &d)
 {
@@ -381,7 +381,7 @@ uint32_t prefill_segments(const janas_attn *a, const SeqDesc &d)
     const uint32_t nt = (d.end - 1) / tile - lo / tile + 1;
     uint64_t want = (a->cus + blocks - 1) / blocks;
     want = std::min<uint64_t>(want, std::max<uint32_t>(1, nt / kSegTiles));
-    return (uint32_t)std::min<uint64_t>(want, kMaxSeg);
+    return (uint32_t)std::min<uint64_t>(want, kMaxSegs);
 }
 
 int run_prefill(janas_attn *a, int kv, int gate_mode,
@@ -412,7 +412,7 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
                 /* partial rows from part0: (token, head) major, segment minor */
                 d.part0 = rows;
                 rows += (uint64_t)d.n * a->n_head * d.nseg;
-                nmg = ((uint64_t)d.n * a->n_head + kPMergeRows - 1) / kPMergeRows;
+                nmg = pmerge_groups(d.n, a->n_head, a->hd);
             }
             if (wg + nwg > 0x7FFFFFFFu || mg + nmg > 0x7FFFFFFFu)
                 return JANAS_ATTN_ERANGE;

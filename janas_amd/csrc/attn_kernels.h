@@ -165,9 +165,17 @@ int prefill_supported(int kv, uint32_t hd);
    per key segment), and the key positions a tile */
 uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd);
 uint32_t prefill_tile(uint32_t hd);
-/* the ordered merge of split sequences' segment partials: n_wg workgroups
-   of kPMergeRows rows (a row is one (token, head)) */
-constexpr uint32_t kPMergeRows = 4;
+/* the ordered merge of split sequences' segment partials: a thread takes 4
+   columns of one row (a row is one (token, head)), a workgroup
+   kPMergeThreads of them; a sequence of n tokens takes pmerge_groups of
+   them */
+constexpr uint32_t kPMergeThreads = 256;
+/* key segments a prefill row block is split into, at most */
+constexpr uint32_t kMaxSegs = 16;
+inline uint64_t pmerge_groups(uint32_t n, uint32_t n_head, uint32_t hd)
+{
+    return ((uint64_t)n * n_head * (hd / 4) + kPMergeThreads - 1) / kPMergeThreads;
+}
 hipError_t launch_prefill_merge(const PrefillArgs &a, uint32_t n_wg, hipStream_t s);
 
 }  // namespace janas

@@ -808,52 +808,77 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
 }
 
 /*
- * The ordered merge of split rows: wave w of workgroup b takes row
- * kPMergeRows b + w of its sequence (a row is one (token, head)), lane t
- * columns 4 t .. 4 t + 3. Segments fold in order against the largest m:
- * out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s, then the gate as in
- * write_out.
+ * The ordered merge of split rows: thread t of workgroup b takes 4 columns
+ * of one row of its sequence (a row is one (token, head)), the pair
+ * kPMergeThreads b + t in row-major order. Up to kPMergeBatch segments'
+ * (m, l) and values are asked for at once (more, one after another), then
+ * folded in segment order against the largest m: out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s, then the gate as
+ * in write_out.
  */
-__global__ __launch_bounds__(kPMergeRows * 64) void pmerge_kernel(const PrefillArgs A)
+constexpr uint32_t kPMergeBatch = 4;
+
+__global__ __launch_bounds__(kPMergeThreads) void pmerge_kernel(const PrefillArgs A)
 {
-    const uint32_t id = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t id = blockIdx.x;
     const uint32_t si = seq_index(A, &SeqDesc::mg0, id);
     const SeqDesc &sq = A.seq[si];
-    const uint32_t hd = A.hd, nseg = sq.nseg;
-    const uint32_t row = (id - sq.mg0) * kPMergeRows + w;
+    const uint32_t hd = A.hd, nseg = sq.nseg, c4 = hd / 4;
+    const uint64_t pair = (uint64_t)(id - sq.mg0) * kPMergeThreads + threadIdx.x;
+    const uint32_t row = (uint32_t)(pair / c4), col = (uint32_t)(pair % c4) * 4;
     if (row >= sq.n * A.n_head)
         return;
     const uint32_t j = row / A.n_head, h = row % A.n_head;
     const size_t pr0 = sq.part0 + (size_t)row * nseg;
-    float mx = -INFINITY;
-    for (uint32_t s = 0; s < nseg; s++)
-        mx = fmaxf(mx, A.part_ml[2 * (pr0 + s)]);
-    /* lane t: columns 4 t .. 4 t + 3, then 256 further (head size 512) */
-    for (uint32_t col = 4 * lane; col < hd; col += 256) {
-        float l = 0.0f;
-        float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint32_t s = 0; s < nseg; s++) {
-            const float2 ml = *(const float2 *)(A.part_ml + 2 * (pr0 + s));
-            const float wt = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - mx);
-            const float4 v = *(const float4 *)(A.part_acc + (pr0 + s) * hd + col);
-            l += wt * ml.y;
-            acc.x += wt * v.x;
-            acc.y += wt * v.y;
-            acc.z += wt * v.z;
-            acc.w += wt * v.w;
-        }
-        const float inv = 1.0f / l;
-        const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
-        float x[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+    float l = 0.0f;
+    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    /* segment s's weight against the largest m, folded in order */
+    auto fold = [&](float mx, float2 ml, float4 v) {
+        const float wt = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - mx);
+        l += wt * ml.y;
+        acc.x += wt * v.x;
+        acc.y += wt * v.y;
+        acc.z += wt * v.z;
+        acc.w += wt * v.w;
+    };
+    if (nseg <= kPMergeBatch) {
+        /* the common case: every segment's loads at once (past nseg the
+           last one again, not used) */
+        float2 ml[kPMergeBatch];
+        float4 v[kPMergeBatch];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            if (A.gate_mode == kGateElem)
-                x[e] *= 1.0f / (1.0f + expf(-sq.gate[oi + e]));
-            else if (A.gate_mode == kGateHead)
-                x[e] *= 1.0f / (1.0f + expf(-sq.gate[(size_t)j * A.n_head + h]));
+        for (uint32_t s = 0; s < kPMergeBatch; s++) {
+            const size_t pr = pr0 + (s < nseg ? s : nseg - 1);
+            ml[s] = *(const float2 *)(A.part_ml + 2 * pr);
+            v[s] = *(const float4 *)(A.part_acc + pr * hd + col);
         }
-        *(float4 *)(sq.out + oi) = float4{x[0], x[1], x[2], x[3]};
+        float mx = -INFINITY;
+#pragma unroll
+        for (uint32_t s = 0; s < kPMergeBatch; s++)
+            if (s < nseg)
+                mx = fmaxf(mx, ml[s].x);
+#pragma unroll
+        for (uint32_t s = 0; s < kPMergeBatch; s++)
+            if (s < nseg)
+                fold(mx, ml[s], v[s]);
+    } else {
+        float mx = -INFINITY;
+        for (uint32_t s = 0; s < nseg; s++)
+            mx = fmaxf(mx, A.part_ml[2 * (pr0 + s)]);
+        for (uint32_t s = 0; s < nseg; s++)
+            fold(mx, *(const float2 *)(A.part_ml + 2 * (pr0 + s)),
+                 *(const float4 *)(A.part_acc + (pr0 + s) * hd + col));
     }
+    const float inv = 1.0f / l;
+    const size_t oi = ((size_t)j * A.n_head + h) * hd + col;
+    float x[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        if (A.gate_mode == kGateElem)
+            x[e] *= 1.0f / (1.0f + expf(-sq.gate[oi + e]));
+        else if (A.gate_mode == kGateHead)
+            x[e] *= 1.0f / (1.0f + expf(-sq.gate[(size_t)j * A.n_head + h]));
+    }
+    *(float4 *)(sq.out + oi) = float4{x[0], x[1], x[2], x[3]};
 }
 
 template <int T, int D>
@@ -895,7 +920,7 @@ uint32_t prefill_tile(uint32_t hd)
 
 hipError_t launch_prefill_merge(const PrefillArgs &a, uint32_t n_wg, hipStream_t s)
 {
-    hipLaunchKernelGGL(pmerge_kernel, dim3(n_wg), dim3(kPMergeRows * 64), 0, s, a);
+    hipLaunchKernelGGL(pmerge_kernel, dim3(n_wg), dim3(kPMergeThreads), 0, s, a);
     return hipGetLastError();
 }
 
