@@ -80,3 +80,61 @@ def test_noalloc_refuses_more_than_the_array(gpu):
             a.run_dev(janas_amd.KV_F16, [dict(k=k, v=k, q=q, out=out, cap=L,
                                               n=64, pos0=L - 64)], path="noalloc")
         assert e.value.code == janas_amd.ERANGE
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """The entry point's reason: code under HIP graph capture. A decode
+    step (f16, gated) and a 16-token block over an int8 cache, captured
+    into one graph through janas_attn_run_dev_noalloc and replayed three
+    times - with eager work in between that overwrites the device's
+    partials array - each replay equal bit for bit to the eager result."""
+    h, kvh, hd, L = 16, 2, 256, 4096
+    k = dev(normal(131, kvh * L * hd).reshape(kvh, L, hd).astype(np.float16), gpu)
+    v = dev(normal(133, kvh * L * hd).reshape(kvh, L, hd).astype(np.float16), gpu)
+    q = dev(normal(137, h * hd).reshape(1, h, hd), gpu)
+    g = dev(normal(139, h * hd).reshape(1, h, hd), gpu)
+    k8 = np.clip(np.rint(normal(141, kvh * L * hd) * 30), -127, 127).astype(np.int8)
+    v8 = np.clip(np.rint(normal(143, kvh * L * hd) * 30), -127, 127).astype(np.int8)
+    ks = dev((0.01 + 0.01 * np.abs(normal(147, kvh * L))).astype(np.float32).reshape(kvh, L), gpu)
+    vs = dev((0.01 + 0.01 * np.abs(normal(149, kvh * L))).astype(np.float32).reshape(kvh, L), gpu)
+    kd, vd = dev(k8.reshape(kvh, L, hd), gpu), dev(v8.reshape(kvh, L, hd), gpu)
+    qb = dev(normal(151, 16 * h * hd).reshape(16, h, hd), gpu)
+    qo = dev(normal(153, 16 * h * hd).reshape(16, h, hd), gpu)
+    want_a, want_b = torch.empty_like(q), torch.empty_like(qb)
+    out_a, out_b = torch.empty_like(q), torch.empty_like(qb)
+    scratch_out = torch.empty_like(qb)
+    s = torch.cuda.Stream()
+    with Attention(h, kvh, hd, L) as a:
+        def calls(oa, ob, path):
+            return [a.prepare(janas_amd.KV_F16, [dict(k=k, v=v, q=q, out=oa, gate=g, cap=L,
+                                                      n=1, pos0=L - 1)],
+                              gate_mode=janas_amd.GATE_ELEM, stream=s.cuda_stream,
+                              path=path),
+                    a.prepare(janas_amd.KV_I8, [dict(k=kd, v=vd, ks=ks, vs=vs, q=qb, out=ob,
+                                                     cap=L, n=16, pos0=L - 16)],
+                              stream=s.cuda_stream, path=path)]
+        with torch.cuda.stream(s):
+            for f in calls(want_a, want_b, "auto"):
+                f()
+            captured = calls(out_a, out_b, "noalloc")
+            for f in captured:   # once outside the capture
+                f()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            for f in captured:
+                f()
+        torch.cuda.synchronize()
+        other = a.prepare(janas_amd.KV_I8, [dict(k=kd, v=vd, ks=ks, vs=vs, q=qo,
+                                                 out=scratch_out, cap=L, n=16, pos0=1000)],
+                          stream=s.cuda_stream, path="noalloc")
+        for _ in range(3):
+            out_a.zero_()
+            out_b.zero_()
+            with torch.cuda.stream(s):
+                other()          # eager: overwrites the partials array
+                graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out_a, want_a)
+            assert torch.equal(out_b, want_b)
+        assert a.status() == 0
