@@ -315,6 +315,12 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
         /* a sequence that asks for Q8_K blocks: the merge takes a block a
            workgroup and quantizes it (the same output bits) */
         args.merge_cols = q8k ? kMergeQ8k : merge_cols(pairs, a->hd);
+        /* row tiles a workgroup, from the launch's largest sequence */
+        const uint32_t tr = split_tile_rows(a->hd);
+        uint64_t tiles = 1;
+        for (uint32_t i = 0; i < m; i++)
+            tiles = std::max<uint64_t>(tiles, ((uint64_t)seqs[s0 + i].n * a->group + tr - 1) / tr);
+        args.mt = split_mt(kv, a->hd, (uint32_t)std::min<uint64_t>(tiles, kSplitMaxMt));
         args.once = 1;
         uint32_t wg = 0, mg = 0;
         /* merge workgroups a (token, head), or a token's blocks */
@@ -328,6 +334,7 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
             d.wg0 = wg;
             d.mg0 = mg;
             d.part0 = rows;
+            d.rtiles = (d.rtiles + args.mt - 1) / args.mt;
             args.once &= d.rtiles == 1;
             uint64_t nwg = (uint64_t)a->n_kv * d.span * d.rtiles;
             uint64_t nmg = q8k ? (uint64_t)d.n * nb : (uint64_t)d.n * a->n_head * nd;

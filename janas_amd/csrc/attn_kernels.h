@@ -28,6 +28,8 @@ constexpr uint32_t kMaxSeqs = 16;
 /* merge workgroups a launch keeps at least when it takes 128 columns a
    workgroup (merge_cols) */
 constexpr uint64_t kMergeFill = 256;
+/* row tiles of kTileRows a split-kernel workgroup takes at most */
+constexpr uint32_t kSplitMaxMt = 2;
 
 enum KvType : int { kI8 = 0, kI16 = 1, kF16 = 2, kF32 = 3 };
 enum GateMode : int { kGateNone = 0, kGateElem = 1, kGateHead = 2 };
@@ -43,8 +45,8 @@ struct SeqDesc {
     const uint32_t *last;  /* [n] or null: token j sees up to pos0 + j */
     uint32_t cap, n, pos0, end; /* end: 1 + the last position any token sees */
     uint32_t c0, span;     /* chunks c0 .. c0 + span - 1 are read */
-    uint32_t rtiles;       /* query-row tiles of split_tile_rows(hd) rows
-                              (rows = n x group) */
+    uint32_t rtiles;       /* workgroups along the query rows (rows = n x
+                              group): of split_tile_rows(hd) x mt rows */
     uint32_t wg0;          /* first workgroup of the split launch */
     uint32_t mg0;          /* first workgroup of the merge launch */
     uint32_t nseg;         /* prefill: key segments a row block is split
@@ -58,7 +60,10 @@ struct SplitArgs {
     float *part_ml;        /* [rows][2]: largest score, sum of weights */
     float *part_acc;       /* [rows][hd]: weighted values */
     uint32_t n_seqs, n_wg;
-    uint32_t once;         /* every sequence one row tile: K/V read once */
+    uint32_t once;         /* every sequence one row workgroup: K/V read
+                              once */
+    uint32_t mt;           /* split kernel: row tiles a workgroup (1 or 2;
+                              split_mt) */
     uint32_t merge_cols;   /* 32 or 128 columns a merge workgroup, or
                               kMergeQ8k: one Q8_K block of 256 outputs */
     uint32_t n_head, n_kv, group, hd, window;
@@ -143,6 +148,9 @@ uint32_t merge_cols(uint64_t pairs, uint32_t hd);
 /* 1 when the split kernel has an instance for this element type and
    padded head size. */
 int split_supported(int kv, uint32_t hd);
+/* row tiles a split-kernel workgroup takes for a launch whose largest
+   sequence has `tiles` row tiles (SplitArgs::mt). */
+uint32_t split_mt(int kv, uint32_t hd, uint32_t tiles);
 /* attn_wide.hip: the split kernel for head sizes 264 .. 512 (8- and 16-bit
    caches); launch_split hands those to it. */
 hipError_t launch_wide(int kv, const SplitArgs &a, hipStream_t s);

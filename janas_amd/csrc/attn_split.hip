@@ -127,23 +127,35 @@ template <int D> __device__ __forceinline__ uint32_t slot(uint32_t u, uint32_t r
    Head sizes up to 128 over 8- and 16-bit caches ask for 3 waves a SIMD
    (at most 168 registers): the f16 instance otherwise takes 176 and holds
    two workgroups a CU, where calls of several row tiles (a verify) or many
-   chunks (a ragged decode) want more in flight. NT:
-   every chunk is read by one workgroup (decode): nontemporal loads; the row
-   tiles of a block of tokens read a chunk each, and plain loads keep it in
-   L2 for them. */
-template <int T, int D, bool NT, bool ONE = false, bool Q16 = false>
+   chunks (a ragged decode) want more in flight. NT: every chunk is read by
+   one workgroup (decode, or a verify whose rows are all one workgroup's):
+   nontemporal loads; the workgroups of a block of tokens read a chunk
+   each, and plain loads keep it in L2 for them.
+   MT: row tiles of 8 a workgroup (1, or 2 at head sizes up to 128 over 8-
+   and 16-bit caches). Every K and V operand read from LDS feeds MT
+   products, one a tile, so a verify's or a block's rows read a chunk once
+   per two tiles. A row's arithmetic - its products, softmax, combine - is
+   the same in either, so its partial is the same bits whichever instance
+   its call takes. */
+template <int T, int D, bool NT, bool ONE = false, bool Q16 = false, int MT = 1>
 __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 128 && T != kF32 ? 3 : 1))) void split_kernel(const SplitArgs A)
 {
     static_assert(!Q16 || (T == kI8 && D % 16 == 0), "INT16: int8 caches");
+    static_assert(MT == 1 || (MT == 2 && D <= 128 && T != kF32),
+                  "two row tiles: 8- and 16-bit rows up to 128");
     using S = SS<T, D>;
     constexpr int KS = S::KS, NT_ = S::NT, LG = S::LG, DP = S::DP;
-    __shared__ __attribute__((aligned(1024))) char sR[kSW * S::REG];
-    __shared__ __attribute__((aligned(16))) _Float16 sQ[16][D + 8];
-    __shared__ float sQs[8];
-    __shared__ __attribute__((aligned(16))) float sM[kSW][8];
-    __shared__ __attribute__((aligned(16))) float sL[kSW][8];
+    constexpr uint32_t TR = kTileRows * MT;      /* query rows a workgroup */
+    /* a wave's LDS region: its staged groups, then its sums (32 D bytes a
+       tile) for the combine */
+    constexpr int CR = S::REG > 32 * D * MT ? S::REG : 32 * D * MT;
+    __shared__ __attribute__((aligned(1024))) char sR[kSW * CR];
+    __shared__ __attribute__((aligned(16))) _Float16 sQ[2 * TR][D + 8];
+    __shared__ float sQs[TR];
+    __shared__ __attribute__((aligned(16))) float sM[kSW][TR];
+    __shared__ __attribute__((aligned(16))) float sL[kSW][TR];
     __shared__ float sPe[kSW];
-    __shared__ float sX[kSW][8];   /* INT16: largest weight x value scale */
+    __shared__ float sX[kSW][TR];   /* INT16: largest weight x value scale */
     __shared__ float sKs[kSW][kSWP], sVs[kSW][kSWP];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -160,12 +172,12 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
     const uint32_t rt = local % sq.rtiles;
     const uint32_t c = sq.c0 + (local / sq.rtiles) % sq.span;
     const uint32_t kvh = local / sq.rtiles / sq.span;
-    const uint32_t R = sq.n * G, r0 = rt * kTileRows;
+    const uint32_t R = sq.n * G, r0 = rt * TR;
     const uint32_t t0 = c * kChunk, plast = sq.end - 1;
 
-    /* the tile's tokens see [lo(first), last(final)]: nothing of this chunk
-       means no partial is needed (the merge does not read it) */
-    const uint32_t rows_here = R - r0 < kTileRows ? R - r0 : kTileRows;
+    /* the workgroup's tokens see [lo(first), last(final)]: nothing of this
+       chunk means no partial is needed (the merge does not read it) */
+    const uint32_t rows_here = R - r0 < TR ? R - r0 : TR;
     const uint32_t jf = r0 / G, jl = (r0 + rows_here - 1) / G;
     const uint32_t lo_all = row_lo(A, sq.pos0 + jf);
     uint32_t hi_all = sq.last ? sq.last[jl] : sq.pos0 + jl;
@@ -178,23 +190,28 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
     const char *const kbase = (const char *)sq.k + crow * rbytes;
     const char *const vbase = (const char *)sq.v + crow * rbytes;
 
-    /* the lane's MFMA row: tile row qr = l16 / 2, plane l16 & 1; its
-       visible positions [rlo, rhi] */
-    const uint32_t qr = l16 >> 1, rq = r0 + qr;
-    const bool qok = rq < R;
-    uint32_t rlo = 1, rhi = 0;
-    if (qok) {
-        const uint32_t j = rq / G;
-        rlo = row_lo(A, sq.pos0 + j);
-        rhi = sq.last ? sq.last[j] : sq.pos0 + j;
-        rhi = rhi < plast ? rhi : plast;
+    /* the lane's MFMA row in tile mt: row qr = l16 / 2 of the tile, plane
+       l16 & 1; its visible positions [rlo, rhi] */
+    const uint32_t qr = l16 >> 1;
+    uint32_t rlo[MT], rhi[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const uint32_t rq = r0 + kTileRows * mt + qr;
+        rlo[mt] = 1;
+        rhi[mt] = 0;
+        if (rq < R) {
+            const uint32_t j = rq / G;
+            rlo[mt] = row_lo(A, sq.pos0 + j);
+            uint32_t hi = sq.last ? sq.last[j] : sq.pos0 + j;
+            rhi[mt] = hi < plast ? hi : plast;
+        }
     }
 
-    /* ---- the query: wave w loads tile rows 2 w, 2 w + 1 (D / 4 lanes a
-       row, a float4 each; columns past hd read column 0) ---- */
+    /* ---- the query: wave w loads rows 2 w, 2 w + 1 of every tile (D / 4
+       lanes a row, a float4 each; columns past hd read column 0) ---- */
     constexpr int QL = D / 4;                  /* lanes a query row */
-    constexpr int QN = QL >= 64 ? 2 : 1;        /* loads a lane */
-    float4 qv[QN];
+    constexpr int QN = QL >= 64 ? 2 : 1;        /* loads a lane a tile */
+    float4 qv[MT][QN];
     uint32_t qrow[QN], qcol[QN];
     /* lanes past the wave's two rows (head size 64) take none */
     const bool qlane = QN == 2 || lane / QL < 2;
@@ -203,11 +220,17 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
         const uint32_t e = QN == 2 ? lane : lane % QL;
         qrow[h] = qlane ? 2 * w + (QN == 2 ? h : lane / QL) : kTileRows;
         qcol[h] = 4 * e;
-        const uint32_t r = r0 + qrow[h] < R ? r0 + qrow[h] : r0;
-        const uint32_t j = r / G, hh = kvh * G + r % G;
-        const float *src = sq.q + ((size_t)j * A.n_head + hh) * hd;
-        qv[h] = *(const float4 *)(src + (qcol[h] < hd ? qcol[h] : 0));
     }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int h = 0; h < QN; h++) {
+            const uint32_t rr = r0 + kTileRows * mt + qrow[h];
+            const uint32_t r = rr < R ? rr : r0;
+            const uint32_t j = r / G, hh = kvh * G + r % G;
+            const float *src = sq.q + ((size_t)j * A.n_head + hh) * hd;
+            qv[mt][h] = *(const float4 *)(src + (qcol[h] < hd ? qcol[h] : 0));
+        }
     /* the value and key scales of the wave's 64 positions, a lane each */
     float ksv = 1.0f, vsv = 1.0f;
     if constexpr (S::SCALED) {
@@ -268,9 +291,13 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
     /* ---- the query planes: scaled by 2^e so that the row's largest |q|
        lies in [2^13, 2^14), split into f16 hi + lo, into LDS ---- */
 #pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
     for (int h = 0; h < QN; h++) {
-        const bool ok = r0 + qrow[h] < R && qrow[h] < kTileRows;
-        const float x[4] = {qv[h].x, qv[h].y, qv[h].z, qv[h].w};
+        const uint32_t tr = kTileRows * mt + qrow[h];   /* row of the workgroup */
+        const bool ok = r0 + tr < R && qrow[h] < kTileRows;
+        const float4 qq = qv[mt][h];
+        const float x[4] = {qq.x, qq.y, qq.z, qq.w};
         float mx = 0.0f;
         if (ok && qcol[h] < hd)
             mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
@@ -285,11 +312,11 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int32_t qi = ok && qcol[h] < hd ? q16_round(x[e], inv) : 0;
-                    sQ[2 * qrow[h]][qcol[h] + e] = (_Float16)(qi >> 8);
-                    sQ[2 * qrow[h] + 1][qcol[h] + e] = (_Float16)(qi & 255);
+                    sQ[2 * tr][qcol[h] + e] = (_Float16)(qi >> 8);
+                    sQ[2 * tr + 1][qcol[h] + e] = (_Float16)(qi & 255);
                 }
                 if (qcol[h] == 0)
-                    sQs[qrow[h]] = mx / 32767.0f;
+                    sQs[tr] = mx / 32767.0f;
             }
             continue;
         }
@@ -304,11 +331,11 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
             for (int e = 0; e < 4; e++) {
                 _Float16 hi, lo;
                 split_hl(ok && qcol[h] < hd ? x[e] * up : 0.0f, hi, lo);
-                sQ[2 * qrow[h]][qcol[h] + e] = hi;
-                sQ[2 * qrow[h] + 1][qcol[h] + e] = lo;
+                sQ[2 * tr][qcol[h] + e] = hi;
+                sQ[2 * tr + 1][qcol[h] + e] = lo;
             }
             if (qcol[h] == 0)
-                sQs[qrow[h]] = ldexpf(1.0f, -ex);
+                sQs[tr] = ldexpf(1.0f, -ex);
         }
     }
     if constexpr (S::SCALED) {
@@ -323,14 +350,18 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
         __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
-    h8 qb[KS];
+    h8 qb[MT][KS];
+    float qs2[MT], qsc[MT];
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++)
-        qb[ks] = *(const h8 *)&sQ[l16][32 * ks + 8 * g];
-    const float qs2 = sQs[qr] * A.scale * kLog2e;
-    const float qsc = sQs[qr];
+    for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++)
+            qb[mt][ks] = *(const h8 *)&sQ[16 * mt + l16][32 * ks + 8 * g];
+        qsc[mt] = sQs[kTileRows * mt + qr];
+        qs2[mt] = qsc[mt] * A.scale * kLog2e;
+    }
 
-    char *const myR = sR + w * S::REG;
+    char *const myR = sR + w * CR;
     /* the group's 16 B of row `row`, byte cb of the padded row, into the
        region (16-bit units; int8 widened, f32 split into two planes) */
     auto stage = [&](const u4 &x0, int l) {
@@ -359,10 +390,14 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
     };
 
     /* ---- scores, a group at a time as its K lands (lane: MFMA row l16 at
-       positions 16 s + 4 g + i) ---- */
+       positions 16 s + 4 g + i), each K operand read once for the MT
+       tiles ---- */
     const uint32_t p0w = t0 + w * kSWP;
-    float sv[kSNG][4];
-    float m = -INFINITY;
+    float sv[MT][kSNG][4];
+    float m[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+        m[mt] = -INFINITY;
 #pragma unroll
     for (int s = 0; s < kSNG; s++) {
         {
@@ -380,7 +415,10 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
                 stage(t[l], l);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        f4 sa = f4{0, 0, 0, 0};
+        f4 sa[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+            sa[mt] = f4{0, 0, 0, 0};
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             h8 ka[DP];
@@ -394,31 +432,36 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
                     ka[1] = *(const h8 *)(myR + S::PLB + l16 * S::LRB + sl);
             }
 #pragma unroll
-            for (int dp = 0; dp < DP; dp++)
-                sa = mfma(ka[dp], qb[ks], sa);
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int dp = 0; dp < DP; dp++)
+                    sa[mt] = mfma(ka[dp], qb[mt][ks], sa[mt]);
         }
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t pl = kSG * s + 4 * g + i, p = p0w + pl;
             float x;
             if constexpr (Q16) {
                 /* natural units, the reference's score bit for bit */
-                const float other = from_x1(sa[i]);
+                const float other = from_x1(sa[mt][i]);
                 const bool odd = l16 & 1;
-                x = q16_score(odd ? other : sa[i], odd ? sa[i] : other, qsc, A.scale,
+                x = q16_score(odd ? other : sa[mt][i], odd ? sa[mt][i] : other, qsc[mt], A.scale,
                               sKs[w][pl]);
             } else {
-                x = (sa[i] + from_x1(sa[i])) * qs2;
+                x = (sa[mt][i] + from_x1(sa[mt][i])) * qs2[mt];
                 if constexpr (S::SCALED)
                     x *= sKs[w][pl];
             }
-            sv[s][i] = p >= rlo && p <= rhi ? x : -INFINITY;
-            m = fmaxf(m, sv[s][i]);
+            sv[mt][s][i] = p >= rlo[mt] && p <= rhi[mt] ? x : -INFINITY;
+            m[mt] = fmaxf(m[mt], sv[mt][s][i]);
         }
     }
-    m = max_x32(max_x16(m));
-
-    h4 pa[kSNG];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+        m[mt] = max_x32(max_x16(m[mt]));
+    h4 pa[MT][kSNG];
     if constexpr (Q16) {
         /* INT16: the chunk's largest score over the 4 waves, the weights
            e^(s - M) times the value scales, their largest over the chunk,
@@ -426,36 +469,46 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
            w >> 8 and w & 255 (att_weights_ref, att_wquant_ref,
            attention.c:158-176, :574-588, :761-772) */
         if (lane < 16 && !(lane & 1))
-            sM[w][lane >> 1] = m;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+                sM[w][kTileRows * mt + (lane >> 1)] = m[mt];
         __syncthreads();
-        m = fmaxf(fmaxf(sM[0][qr], sM[1][qr]), fmaxf(sM[2][qr], sM[3][qr]));
-        const float mm = m == -INFINITY ? 0.0f : m;
-        float pv[kSNG][4];
-        float lsum = 0.0f, vmx = 0.0f;
+        float pv[MT][kSNG][4];
 #pragma unroll
-        for (int s = 0; s < kSNG; s++)
+        for (int mt = 0; mt < MT; mt++) {
+            const uint32_t rr = kTileRows * mt + qr;
+            m[mt] = fmaxf(fmaxf(sM[0][rr], sM[1][rr]), fmaxf(sM[2][rr], sM[3][rr]));
+            const float mm = m[mt] == -INFINITY ? 0.0f : m[mt];
+            float lsum = 0.0f, vmx = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float wt = det_weight(sv[s][i], mm);
-                lsum += wt;
-                pv[s][i] = wt * sVs[w][kSG * s + 4 * g + i];
-                vmx = fmaxf(vmx, pv[s][i]);
+            for (int s = 0; s < kSNG; s++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float wt = det_weight(sv[mt][s][i], mm);
+                    lsum += wt;
+                    pv[mt][s][i] = wt * sVs[w][kSG * s + 4 * g + i];
+                    vmx = fmaxf(vmx, pv[mt][s][i]);
+                }
+            vmx = max_x32(max_x16(vmx));
+            lsum = sum_x32(sum_x16(lsum));
+            if (lane < 16 && !(lane & 1)) {
+                sX[w][kTileRows * mt + (lane >> 1)] = vmx;
+                sL[w][kTileRows * mt + (lane >> 1)] = lsum;
             }
-        vmx = max_x32(max_x16(vmx));
-        lsum = sum_x32(sum_x16(lsum));
-        if (lane < 16 && !(lane & 1)) {
-            sX[w][lane >> 1] = vmx;
-            sL[w][lane >> 1] = lsum;
         }
         __syncthreads();
-        const float inv = q16_inv(fmaxf(fmaxf(sX[0][qr], sX[1][qr]), fmaxf(sX[2][qr], sX[3][qr])));
 #pragma unroll
-        for (int s = 0; s < kSNG; s++)
+        for (int mt = 0; mt < MT; mt++) {
+            const uint32_t rr = kTileRows * mt + qr;
+            const float inv = q16_inv(fmaxf(fmaxf(sX[0][rr], sX[1][rr]), fmaxf(sX[2][rr], sX[3][rr])));
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int32_t q = q16_round(pv[s][i], inv);
-                pa[s][i] = (l16 & 1) ? (_Float16)(q & 255) : (_Float16)(q >> 8);
-            }
+            for (int s = 0; s < kSNG; s++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int32_t q = q16_round(pv[mt][s][i], inv);
+                    pa[mt][s][i] = (l16 & 1) ? (_Float16)(q & 255) : (_Float16)(q >> 8);
+                }
+        }
     }
 
     /* ---- the wave's softmax (powers of two); the weights' power of two
@@ -476,36 +529,42 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
     }
     if constexpr (!Q16) {
         const float up = ldexpf(1.0f, pe);
-        const float mm = m == -INFINITY ? 0.0f : m;
-        float lsum = 0.0f;
 #pragma unroll
-        for (int s = 0; s < kSNG; s++)
+        for (int mt = 0; mt < MT; mt++) {
+            const float mm = m[mt] == -INFINITY ? 0.0f : m[mt];
+            float lsum = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float d = sv[s][i] - mm;
-                const float pw = d >= kCut2 ? __builtin_amdgcn_exp2f(d) : 0.0f;
-                lsum += pw;
-                float pv = pw * up;
-                if constexpr (S::SCALED)
-                    pv *= sVs[w][kSG * s + 4 * g + i];
-                _Float16 hi, lo;
-                split_hl(pv, hi, lo);
-                pa[s][i] = (l16 & 1) ? lo : hi;
+            for (int s = 0; s < kSNG; s++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float d = sv[mt][s][i] - mm;
+                    const float pw = d >= kCut2 ? __builtin_amdgcn_exp2f(d) : 0.0f;
+                    lsum += pw;
+                    float pv = pw * up;
+                    if constexpr (S::SCALED)
+                        pv *= sVs[w][kSG * s + 4 * g + i];
+                    _Float16 hi, lo;
+                    split_hl(pv, hi, lo);
+                    pa[mt][s][i] = (l16 & 1) ? lo : hi;
+                }
+            lsum = sum_x32(sum_x16(lsum));
+            if (lane < 16 && !(lane & 1)) {
+                sM[w][kTileRows * mt + (lane >> 1)] = m[mt];
+                sL[w][kTileRows * mt + (lane >> 1)] = lsum;
             }
-        lsum = sum_x32(sum_x16(lsum));
-        if (lane < 16 && !(lane & 1)) {
-            sM[w][lane >> 1] = m;
-            sL[w][lane >> 1] = lsum;
         }
         if (lane == 0)
             sPe[w] = ldexpf(1.0f, -pe);
     }
 
-    /* ---- values, a group at a time as its V lands ---- */
-    f4 o[NT_];
+    /* ---- values, a group at a time as its V lands, each V operand read
+       once for the MT tiles ---- */
+    f4 o[MT][NT_];
 #pragma unroll
-    for (int t = 0; t < NT_; t++)
-        o[t] = f4{0, 0, 0, 0};
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int t = 0; t < NT_; t++)
+            o[mt][t] = f4{0, 0, 0, 0};
     const uint32_t r1 = 4 * g + (l16 >> 2);
 #pragma unroll
     for (int s = 0; s < kSNG; s++) {
@@ -545,88 +604,99 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
             }
         }
 #pragma unroll
-        for (int t = 0; t < NT_; t++)
+        for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-            for (int dp = 0; dp < DP; dp++)
-                o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[s], vb[t][dp], o[t], 0, 0, 0);
+            for (int t = 0; t < NT_; t++)
+#pragma unroll
+                for (int dp = 0; dp < DP; dp++)
+                    o[mt][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[mt][s], vb[t][dp], o[mt][t], 0, 0, 0);
     }
 
     /* ---- the waves combined: tile row 2 g + h's sums are o[t][2 h] +
        o[t][2 h + 1] (high and low weights); into the region, then wave w
-       sums its tiles over the waves with weights 2^(m_w - M) 2^-pe_w ---- */
+       sums its column tiles over the waves with weights 2^(m_w - M)
+       2^-pe_w ---- */
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     float2 *mine = (float2 *)myR;
-#pragma unroll
-    for (int t = 0; t < NT_; t++) {
-        if constexpr (Q16) {
-            /* exact integer sums, 256 hi + lo as int32 bits (at most 64
-               positions of 32767 x 128: no overflow) */
-            const int32_t a0 = (int32_t)o[t][0] * 256 + (int32_t)o[t][1];
-            const int32_t a1 = (int32_t)o[t][2] * 256 + (int32_t)o[t][3];
-            mine[t * 64 + lane] = make_float2(__int_as_float(a0), __int_as_float(a1));
-        } else {
-            mine[t * 64 + lane] = make_float2(o[t][0] + o[t][1], o[t][2] + o[t][3]);
-        }
-    }
-    __syncthreads();
-    const uint64_t prow = sq.part0 + ((uint64_t)kvh * sq.span + (c - sq.c0)) * R + r0;
+    const uint64_t prow0 = sq.part0 + ((uint64_t)kvh * sq.span + (c - sq.c0)) * R + r0;
+    /* lane jj of a tile: source lanes 2 jj, 2 jj + 1 - tile rows 2 gs,
+       2 gs + 1 of columns cs, cs + 1 */
+    const uint32_t jj = lane & 31, gs = jj >> 3;
     {
-        /* lane jj of a tile: source lanes 2 jj, 2 jj + 1 - tile rows 2 gs,
-           2 gs + 1 of columns cs, cs + 1 */
-        const uint32_t jj = lane & 31, gs = jj >> 3;
-        float fw[kSW][2], wsc[2];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int t = 0; t < NT_; t++) {
             if constexpr (Q16) {
-                /* the weights' scale, mx / 32767 (att_wquant_ref) */
-                const uint32_t rr = 2 * gs + h;
-                wsc[h] = fmaxf(fmaxf(sX[0][rr], sX[1][rr]), fmaxf(sX[2][rr], sX[3][rr])) / 32767.0f;
-                continue;
-            }
-            float mc = -INFINITY;
-#pragma unroll
-            for (int ww = 0; ww < kSW; ww++)
-                mc = fmaxf(mc, sM[ww][2 * gs + h]);
-#pragma unroll
-            for (int ww = 0; ww < kSW; ww++) {
-                const float mw = sM[ww][2 * gs + h];
-                fw[ww][h] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mc) * sPe[ww];
+                /* exact integer sums, 256 hi + lo as int32 bits (at most 64
+                   positions of 32767 x 128: no overflow) */
+                const int32_t a0 = (int32_t)o[mt][t][0] * 256 + (int32_t)o[mt][t][1];
+                const int32_t a1 = (int32_t)o[mt][t][2] * 256 + (int32_t)o[mt][t][3];
+                mine[(mt * NT_ + t) * 64 + lane] = make_float2(__int_as_float(a0), __int_as_float(a1));
+            } else {
+                mine[(mt * NT_ + t) * 64 + lane] =
+                    make_float2(o[mt][t][0] + o[mt][t][1], o[mt][t][2] + o[mt][t][3]);
             }
         }
-        constexpr int TPW = NT_ / kSW;   /* tiles a wave: 1, 2 or 4 */
+        __syncthreads();
 #pragma unroll
-        for (int tt = 0; tt < (TPW + 1) / 2; tt++) {
-            const uint32_t t = TPW * w + 2 * tt + (lane >> 5);
-            if (TPW == 1 && lane >= 32)
-                break;
-            const uint32_t cs = 16 * t + ((2 * jj) & 15);
-            f4 part[kSW];
+        for (int mt = 0; mt < MT; mt++) {
+            const uint32_t rb = kTileRows * mt;   /* the tile's first row */
+            float fw[kSW][2], wsc[2];
 #pragma unroll
-            for (int ww = 0; ww < kSW; ww++)
-                part[ww] = ((const f4 *)(sR + ww * S::REG))[t * 32 + jj];
-            float res[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int h = 0; h < 2; h++) {
+                const uint32_t rr = rb + 2 * gs + h;
                 if constexpr (Q16) {
-                    /* the chunk's exact int32 sum, then one multiply
-                       (att_values_i16_ref, attention.c:178-193) */
-                    const int32_t acc = (__float_as_int(part[0][i]) + __float_as_int(part[1][i])) +
-                                        (__float_as_int(part[2][i]) + __float_as_int(part[3][i]));
-                    res[i] = (float)acc * wsc[i % 2];
-                } else {
-                    res[i] = (part[0][i] * fw[0][i % 2] + part[1][i] * fw[1][i % 2]) +
-                             (part[2][i] * fw[2][i % 2] + part[3][i] * fw[3][i % 2]);
+                    /* the weights' scale, mx / 32767 (att_wquant_ref) */
+                    wsc[h] = fmaxf(fmaxf(sX[0][rr], sX[1][rr]), fmaxf(sX[2][rr], sX[3][rr])) / 32767.0f;
+                    continue;
+                }
+                float mx = -INFINITY;
+#pragma unroll
+                for (int ww = 0; ww < kSW; ww++)
+                    mx = fmaxf(mx, sM[ww][rr]);
+#pragma unroll
+                for (int ww = 0; ww < kSW; ww++) {
+                    const float mw = sM[ww][rr];
+                    fw[ww][h] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mx) * sPe[ww];
                 }
             }
-            if (cs < hd) {
-                if (r0 + 2 * gs < R)
-                    *(float2 *)&A.part_acc[(prow + 2 * gs) * hd + cs] = make_float2(res[0], res[2]);
-                if (r0 + 2 * gs + 1 < R)
-                    *(float2 *)&A.part_acc[(prow + 2 * gs + 1) * hd + cs] = make_float2(res[1], res[3]);
+            constexpr int TPW = NT_ / kSW;   /* column tiles a wave: 1, 2 or 4 */
+#pragma unroll
+            for (int tt = 0; tt < (TPW + 1) / 2; tt++) {
+                const uint32_t t = TPW * w + 2 * tt + (lane >> 5);
+                if (TPW == 1 && lane >= 32)
+                    break;
+                const uint32_t cs = 16 * t + ((2 * jj) & 15);
+                f4 part[kSW];
+#pragma unroll
+                for (int ww = 0; ww < kSW; ww++)
+                    part[ww] = ((const f4 *)(sR + ww * CR))[(mt * NT_ + t) * 32 + jj];
+                float res[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if constexpr (Q16) {
+                        /* the chunk's exact int32 sum, then one multiply
+                           (att_values_i16_ref, attention.c:178-193) */
+                        const int32_t acc = (__float_as_int(part[0][i]) + __float_as_int(part[1][i])) +
+                                            (__float_as_int(part[2][i]) + __float_as_int(part[3][i]));
+                        res[i] = (float)acc * wsc[i % 2];
+                    } else {
+                        res[i] = (part[0][i] * fw[0][i % 2] + part[1][i] * fw[1][i % 2]) +
+                                 (part[2][i] * fw[2][i % 2] + part[3][i] * fw[3][i % 2]);
+                    }
+                }
+                if (cs < hd) {
+                    const uint32_t ra = rb + 2 * gs;
+                    if (r0 + ra < R)
+                        *(float2 *)&A.part_acc[(prow0 + ra) * hd + cs] = make_float2(res[0], res[2]);
+                    if (r0 + ra + 1 < R)
+                        *(float2 *)&A.part_acc[(prow0 + ra + 1) * hd + cs] = make_float2(res[1], res[3]);
+                }
             }
         }
     }
-    if (w == 0 && lane < kTileRows && r0 + lane < R) {
+    if (w == 0 && lane < TR && r0 + lane < R) {
         float mc = -INFINITY;
 #pragma unroll
         for (int ww = 0; ww < kSW; ww++)
@@ -644,7 +714,7 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
            the merge */
         if constexpr (Q16)
             mc *= kLog2e;
-        *(float2 *)&A.part_ml[(prow + lane) * 2] = make_float2(mc, (l[0] + l[1]) + (l[2] + l[3]));
+        *(float2 *)&A.part_ml[(prow0 + lane) * 2] = make_float2(mc, (l[0] + l[1]) + (l[2] + l[3]));
     }
 }
 
@@ -852,27 +922,38 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     }
 }
 
+template <int T, int D, bool Q16, int MT>
+hipError_t launch_m(const SplitArgs &a, hipStream_t s)
+{
+    if (a.once && a.n_seqs == 1)
+        hipLaunchKernelGGL((split_kernel<T, D, true, true, Q16, MT>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
+    else if (a.once)
+        hipLaunchKernelGGL((split_kernel<T, D, true, false, Q16, MT>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
+    else
+        hipLaunchKernelGGL((split_kernel<T, D, false, false, Q16, MT>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int T, int D, bool Q16>
+hipError_t launch_q(const SplitArgs &a, hipStream_t s)
+{
+    if constexpr (D <= 128 && T != kF32) {
+        if (a.mt == 2)
+            return launch_m<T, D, Q16, 2>(a, s);
+    }
+    if (a.mt != 1)
+        return hipErrorInvalidValue;
+    return launch_m<T, D, Q16, 1>(a, s);
+}
+
 template <int T, int D>
 hipError_t launch_t(const SplitArgs &a, hipStream_t s)
 {
     if constexpr (T == kI8 && D % 16 == 0) {
-        if (a.int16) {
-            if (a.once && a.n_seqs == 1)
-                hipLaunchKernelGGL((split_kernel<T, D, true, true, true>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
-            else if (a.once)
-                hipLaunchKernelGGL((split_kernel<T, D, true, false, true>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
-            else
-                hipLaunchKernelGGL((split_kernel<T, D, false, false, true>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
-            return hipGetLastError();
-        }
+        if (a.int16)
+            return launch_q<T, D, true>(a, s);
     }
-    if (a.once && a.n_seqs == 1)
-        hipLaunchKernelGGL((split_kernel<T, D, true, true>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
-    else if (a.once)
-        hipLaunchKernelGGL((split_kernel<T, D, true>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
-    else
-        hipLaunchKernelGGL((split_kernel<T, D, false>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
-    return hipGetLastError();
+    return launch_q<T, D, false>(a, s);
 }
 
 template <int T>
@@ -899,6 +980,23 @@ int split_supported(int kv, uint32_t hd)
        row is read 16 bytes at a time, so it needs 16 bytes at least. */
     return kv >= kI8 && kv <= kF32 && hd >= (kv == kI8 ? 16u : 8u) && hd % 8 == 0 &&
            hd <= (kv == kF32 ? 128u : 512u);
+}
+
+uint32_t split_mt(int kv, uint32_t hd, uint32_t tiles)
+{
+    /* row tiles a workgroup: two when a KV head's rows fill them, for 8-
+       and 16-bit rows up to 128 numbers. Four (one workgroup for a verify's
+       32 rows) measured slower than two: each wave's chain of products and
+       softmax grows with its tiles, and this kernel is bound by that chain,
+       not by the matrix cores' rate (8 drafts over 8k positions, 32 / 8 /
+       128: one tile 15.1 us, two 14.1, four 16.2). Above 128 the sums of
+       two tiles would not fit beside the staged rows. */
+    if (kv == kF32 || hd > 128)
+        return 1;
+    uint32_t mt = 1;
+    while (mt < tiles && mt < kSplitMaxMt)
+        mt *= 2;
+    return mt;
 }
 
 hipError_t launch_split(int kv, const SplitArgs &a, hipStream_t s)

@@ -259,13 +259,14 @@ def normal_cache(seed, count):
     return normal(seed, count)
 
 
-def run_block(c, kv, gpu, pos0, window=0, last=None, per_token=False):
+def run_block(c, kv, gpu, pos0, window=0, last=None, per_token=False,
+              scores=janas_amd.AUTO):
     d = dict(k=to_dev(c["k"], gpu), v=to_dev(c["v"], gpu),
              q=to_dev(c["q"], gpu), cap=c["L"], n=c["n"], pos0=pos0)
     if c["ks"] is not None:
         d["ks"], d["vs"] = to_dev(c["ks"], gpu), to_dev(c["vs"], gpu)
     d["out"] = torch.zeros(d["q"].shape, dtype=torch.float32, device=gpu)
-    with Attention(c["h"], c["n_kv"], c["hd"], c["L"]) as a:
+    with Attention(c["h"], c["n_kv"], c["hd"], c["L"], 1, scores) as a:
         if window:
             a.set_window(window)
         if not per_token:
@@ -302,6 +303,38 @@ def test_large_block_equals_tokens(kv, gpu):
         1.0, float(np.abs(ref).max()))
     print(f"kv {kv}: large block max abs err {err:.2e} (bar {bar:.1e})")
     assert within(err, bar, "vs oracle")
+
+
+# (cache, heads, KV heads, head size, tokens, scores): a KV head's rows fill
+# two 8-row tiles only in part (15, 12, 9 and 16 rows), so one workgroup
+# takes both, while a token alone (at most 8 rows) takes one tile a
+# workgroup
+TWO_TILES = [(KV_F16, 6, 2, 64, 5, janas_amd.FLOAT),
+             (KV_F16, 4, 4, 128, 12, janas_amd.FLOAT),
+             (KV_I8, 12, 4, 128, 3, janas_amd.FLOAT),
+             (KV_I16, 16, 2, 64, 2, janas_amd.FLOAT),
+             (KV_I8, 6, 2, 128, 5, janas_amd.INT16),
+             (KV_I8, 8, 1, 64, 2, janas_amd.INT16)]
+
+
+@pytest.mark.parametrize("kv,h,n_kv,hd,n,scores", TWO_TILES)
+def test_two_tile_workgroups_equal_tokens(kv, h, n_kv, hd, n, scores, gpu):
+    """Blocks whose rows take the two-tile workgroups, the second tile only
+    partly filled, equal their tokens run one at a time (one-tile
+    workgroups) bit for bit; FLOAT blocks against the restatement too."""
+    c = block_case(kv, n_kv=n_kv, h=h, hd=hd, L=1000, n=n, seed=8400 + h + hd + n)
+    pos0 = c["L"] - n
+    blk = run_block(c, kv, gpu, pos0, scores=scores)
+    one = run_block(c, kv, gpu, pos0, per_token=True, scores=scores)
+    assert np.array_equal(blk.view(np.int32), one.view(np.int32))
+    ref = orc.run(c["q"], c["k"], c["v"], c["ks"], c["vs"], n_head=h,
+                  n_kv=n_kv, hd=hd, pos0=pos0, kv=kv, threads=16,
+                  int16=scores == janas_amd.INT16)
+    err = abs_err(blk, ref)
+    bar = TOL_F16_ABS if kv == KV_F16 else TOL_FLOAT_ABS * max(
+        1.0, float(np.abs(ref).max()))
+    print(f"two tiles kv {kv} {h}/{n_kv}/{hd} n {n} scores {scores}: max abs err {err:.2e}")
+    assert within(err, bar, "two-tile block vs oracle")
 
 
 def test_large_block_window_and_last(gpu):
