@@ -371,89 +371,121 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
 
 /* Key segments for a prefill sequence whose row blocks alone would leave
    compute units idle (a short prompt, a chunk of a long one): enough to
-   give each unit a workgroup, at least kSegTiles key tiles each. It
-   depends on the sequence alone, so a sequence's result is the same in
-   any launch. */
+   give each unit a workgroup, at least kSegTiles key tiles each (twice as
+   many with the halves' tiles, which two groups share). It depends on the
+   sequence alone, so a sequence's result is the same in any launch. */
 constexpr uint32_t kSegTiles = 6;
 
-uint32_t prefill_segments(const janas_attn *a, const SeqDesc &d)
+uint32_t prefill_segments(const janas_attn *a, const SeqDesc &d, bool halves)
 {
-    const uint64_t blocks = (uint64_t)a->n_kv * prefill_row_blocks(d.n, a->group, a->hd);
+    const uint64_t blocks =
+        (uint64_t)a->n_kv * prefill_row_blocks(d.n, a->group, a->hd, halves);
     if (blocks >= a->cus)
         return 1;
     /* the key tiles of the latest row block, which sees the most */
-    const uint32_t tile = prefill_tile(a->hd);
+    const uint32_t tile = prefill_tile(a->hd, halves);
     const uint32_t last = d.pos0 + d.n - 1;
     const uint32_t lo = a->window && last + 1 > a->window ? last + 1 - a->window : 0;
     const uint32_t nt = (d.end - 1) / tile - lo / tile + 1;
+    const uint32_t min_tiles = halves ? 2 * kSegTiles : kSegTiles;
     uint64_t want = (a->cus + blocks - 1) / blocks;
-    want = std::min<uint64_t>(want, std::max<uint32_t>(1, nt / kSegTiles));
+    want = std::min<uint64_t>(want, std::max<uint32_t>(1, nt / min_tiles));
     return (uint32_t)std::min<uint64_t>(want, kMaxSegs);
 }
 
+/* Whether a prefill sequence takes the two-halves kernel (128 rows a
+   workgroup as two key groups, prefill_half_kernel): f16 rows of 72..128
+   numbers whose workgroups in the DMA kernel, key segments included, would
+   still leave compute units idle - a prompt of about a thousand tokens, or
+   an early chunk of a chunked prefill, whose key range is too short to cut
+   into segments. Where segments fill the GPU the DMA kernel stays: its
+   128-position tiles are cheaper a position than the halves' 64. It
+   depends on the sequence alone, so a sequence's result is the same in any
+   launch. */
+bool prefill_halves(const janas_attn *a, int kv, const SeqDesc &d)
+{
+    if (!prefill_halves_supported(kv, a->hd))
+        return false;
+    const uint64_t wg = (uint64_t)a->n_kv * prefill_segments(a, d, false) *
+                        prefill_row_blocks(d.n, a->group, a->hd, false);
+    return wg < a->cus;
+}
+
+/* The sequences in launches of up to kMaxSeqs, those that take the
+   two-halves kernel first, then the others. */
 int run_prefill(janas_attn *a, int kv, int gate_mode,
                 const janas_attn_seq *seqs, uint32_t n_seqs, hipStream_t stream,
                 bool fixed = false)
 {
     if (!prefill_supported(kv, a->hd))
         return JANAS_ATTN_ENOTSUP;
-    for (uint32_t s0 = 0; s0 < n_seqs; s0 += kMaxSeqs) {
-        uint32_t m = std::min(kMaxSeqs, n_seqs - s0);
-        PrefillArgs args;
-        memset(&args, 0, sizeof args);
-        uint32_t wg = 0, mg = 0;
-        uint64_t rows = 0;
-        for (uint32_t i = 0; i < m; i++) {
-            SeqDesc &d = args.seq[i];
-            int rc = describe(a, kv, seqs[s0 + i], d);
-            if (rc)
-                return rc;
-            d.wg0 = wg;
-            d.mg0 = mg;
-            d.nseg = prefill_segments(a, d);
-            d.part0 = 0;
-            uint64_t nwg = (uint64_t)a->n_kv * d.nseg *
-                           prefill_row_blocks(d.n, a->group, a->hd);
-            uint64_t nmg = 0;
-            if (d.nseg > 1) {
-                /* partial rows from part0: (token, head) major, segment minor */
-                d.part0 = rows;
-                rows += (uint64_t)d.n * a->n_head * d.nseg;
-                nmg = pmerge_groups(d.n, a->n_head, a->hd);
+    for (int hv = 1; hv >= 0; hv--) {
+        for (uint32_t i = 0; i < n_seqs;) {
+            PrefillArgs args;
+            memset(&args, 0, sizeof args);
+            const janas_attn_seq *picked[kMaxSeqs];
+            uint32_t m = 0, wg = 0, mg = 0;
+            uint64_t rows = 0;
+            for (; i < n_seqs && m < kMaxSeqs; i++) {
+                SeqDesc &d = args.seq[m];
+                int rc = describe(a, kv, seqs[i], d);
+                if (rc)
+                    return rc;
+                if (prefill_halves(a, kv, d) != (hv == 1))
+                    continue;
+                d.wg0 = wg;
+                d.mg0 = mg;
+                d.nseg = prefill_segments(a, d, hv == 1);
+                d.part0 = 0;
+                uint64_t nwg = (uint64_t)a->n_kv * d.nseg *
+                               prefill_row_blocks(d.n, a->group, a->hd, hv == 1);
+                uint64_t nmg = 0;
+                if (d.nseg > 1) {
+                    /* partial rows from part0: (token, head) major, segment minor */
+                    d.part0 = rows;
+                    rows += (uint64_t)d.n * a->n_head * d.nseg;
+                    nmg = pmerge_groups(d.n, a->n_head, a->hd);
+                }
+                if (wg + nwg > 0x7FFFFFFFu || mg + nmg > 0x7FFFFFFFu)
+                    return JANAS_ATTN_ERANGE;
+                wg += (uint32_t)nwg;
+                mg += (uint32_t)nmg;
+                picked[m++] = &seqs[i];
             }
-            if (wg + nwg > 0x7FFFFFFFu || mg + nmg > 0x7FFFFFFFu)
-                return JANAS_ATTN_ERANGE;
-            wg += (uint32_t)nwg;
-            mg += (uint32_t)nmg;
+            if (m == 0)
+                break;
+            Parts pt{nullptr, nullptr, fixed};
+            if (rows) {
+                int rc = get_parts(a, rows, stream, fixed, pt);
+                if (rc)
+                    return rc;
+            }
+            args.part_ml = pt.ml;
+            args.part_acc = pt.acc;
+            args.n_seqs = m;
+            args.n_wg = wg;
+            args.n_head = a->n_head;
+            args.n_kv = a->n_kv;
+            args.group = a->group;
+            args.hd = a->hd;
+            args.window = a->window;
+            args.scale = a->scale;
+            args.ring = a->ring;
+            args.gate_mode = gate_mode;
+            args.halves = hv;
+            ProfEv *ev = fixed ? nullptr : prof_begin(a, 2, stream);
+            hipError_t e = launch_prefill(kv, args, stream);
+            if (e == hipSuccess && mg)
+                e = launch_prefill_merge(args, mg, stream);
+            prof_end(ev, stream);
+            if (e != hipSuccess)
+                return hip_err(e, "prefill launch");
+            for (uint32_t j = 0; j < m; j++) {
+                int rc = put_q8k(a, picked[j], 1, stream);
+                if (rc)
+                    return rc;
+            }
         }
-        Parts pt{nullptr, nullptr, fixed};
-        if (rows) {
-            int rc = get_parts(a, rows, stream, fixed, pt);
-            if (rc)
-                return rc;
-        }
-        args.part_ml = pt.ml;
-        args.part_acc = pt.acc;
-        args.n_seqs = m;
-        args.n_wg = wg;
-        args.n_head = a->n_head;
-        args.n_kv = a->n_kv;
-        args.group = a->group;
-        args.hd = a->hd;
-        args.window = a->window;
-        args.scale = a->scale;
-        args.ring = a->ring;
-        args.gate_mode = gate_mode;
-        ProfEv *ev = fixed ? nullptr : prof_begin(a, 2, stream);
-        hipError_t e = launch_prefill(kv, args, stream);
-        if (e == hipSuccess && mg)
-            e = launch_prefill_merge(args, mg, stream);
-        prof_end(ev, stream);
-        if (e != hipSuccess)
-            return hip_err(e, "prefill launch");
-        int rc = put_q8k(a, seqs + s0, m, stream);
-        if (rc)
-            return rc;
     }
     return JANAS_ATTN_OK;
 }

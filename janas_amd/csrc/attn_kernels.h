@@ -85,6 +85,8 @@ struct PrefillArgs {
     float scale;
     int ring;
     int gate_mode;
+    int halves;            /* the two-halves kernel (prefill_halves_supported):
+                              128 rows a workgroup, two key groups */
 };
 
 /* Rows of a cache write or of the query preparation (attn_cache.hip). */
@@ -170,9 +172,12 @@ void *scratch_ptr(int dev);
 hipError_t launch_prefill(int kv, const PrefillArgs &a, hipStream_t s);
 int prefill_supported(int kv, uint32_t hd);
 /* row blocks a KV head of an n-token sequence takes (one workgroup each
-   per key segment), and the key positions a tile */
-uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd);
-uint32_t prefill_tile(uint32_t hd);
+   per key segment), and the key positions a tile; halves: the two-halves
+   kernel's (PrefillArgs::halves) */
+uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd, bool halves);
+uint32_t prefill_tile(uint32_t hd, bool halves);
+/* 1 when the two-halves kernel takes this element type and head size */
+int prefill_halves_supported(int kv, uint32_t hd);
 /* the ordered merge of split sequences' segment partials: a thread takes 4
    columns of one row (a row is one (token, head)), a workgroup
    kPMergeThreads of them; a sequence of n tokens takes pmerge_groups of

@@ -85,13 +85,19 @@ constexpr int kPRows = 32;                 /* query rows a wave */
    softmax, each the value product and the output of 256 columns, over
    32-position tiles; each takes the score product over its own 256 columns
    of the head and the two partial scores meet in LDS */
-template <int D> struct PCfg {
+/* HV (halves, head sizes 72..128, calls whose row blocks would leave
+   compute units idle): the 8 waves are two key groups of 4 over the same
+   128 rows, each taking half of the block's key tiles of 64 positions; the
+   two halves' states are combined in LDS at the end */
+template <int D, bool HV = false> struct PCfg {
+    static_assert(!HV || D == 128, "halves: head sizes 72..128");
     static constexpr int W = D > 128 ? 4 : 8;
-    static constexpr int TILE = D > 256 ? 32 : D > 128 ? 64 : 128;
+    static constexpr int GW = HV ? 4 : W;   /* waves a key group */
+    static constexpr int TILE = HV ? 64 : D > 256 ? 32 : D > 128 ? 64 : 128;
     static constexpr int NPB = TILE / 32;   /* blocks of 32 positions a tile */
     static constexpr int CS = D > 256 ? 2 : 1;  /* column splits of a row */
     static constexpr int OC = D / CS;       /* output columns a wave */
-    static constexpr int BLOCK = W / CS * kPRows; /* query rows a workgroup */
+    static constexpr int BLOCK = GW / CS * kPRows; /* query rows a workgroup */
 };
 constexpr float kLog2e = 1.4426950408889634f;
 /* a row's weights are exp2(s - m) against a maximum m that is only moved
@@ -212,10 +218,10 @@ struct PBlock {
     uint32_t col0;             /* the wave's first output column */
 };
 
-template <int D>
+template <int D, bool HV = false>
 __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
 {
-    constexpr int kPBlock = PCfg<D>::BLOCK, kTile = PCfg<D>::TILE;
+    constexpr int kPBlock = PCfg<D, HV>::BLOCK, kTile = PCfg<D, HV>::TILE;
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t l32 = lane & 31;
     const uint32_t id = xcd_remap(blockIdx.x, gridDim.x);
@@ -260,7 +266,7 @@ __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
     }
     P.head_row = (size_t)kvh * sq.cap;
 
-    const uint32_t r = r0 + kPRows * (w / PCfg<D>::CS) + l32;
+    const uint32_t r = r0 + kPRows * ((w % PCfg<D, HV>::GW) / PCfg<D>::CS) + l32;
     P.col0 = (w % PCfg<D>::CS) * PCfg<D>::OC;
     P.rok = r < R;
     P.rj = (P.rok ? r : r0) / G;
@@ -294,7 +300,7 @@ __device__ __forceinline__ void load_query(const PrefillArgs &A, const PBlock &P
 }
 
 /*
- * One key tile of 128 positions from p0 for the lane's row: the scores,
+ * One key tile (PCfg::TILE positions) from p0 for the lane's row: the scores,
  * the masks, the lazy-maximum softmax and the value product. kop(s, b) is
  * the A operand of score k-step s for positions 32 b .. 32 b + 31 (K rows
  * 32 b + l % 32, columns 16 s + 8 (l / 32) .. + 7); vop(ks, c) the A operand
@@ -305,12 +311,12 @@ struct NoExchange {
     template <class T> __device__ void operator()(T *) const {}
 };
 
-template <int D, bool PIPE, class KOp, class VOp, class XOp = NoExchange>
+template <int D, bool PIPE, bool HV = false, class KOp, class VOp, class XOp = NoExchange>
 __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8 *qb,
                                           float &m, float &lsum, f16x *o,
                                           KOp kop, VOp vop, XOp xop = XOp())
 {
-    constexpr int kNPB = PCfg<D>::NPB, kTile = PCfg<D>::TILE;
+    constexpr int kNPB = PCfg<D, HV>::NPB, kTile = PCfg<D, HV>::TILE;
     constexpr int KS = D / 16 / PCfg<D>::CS, CT = PCfg<D>::OC / 32;
     const uint32_t g = (threadIdx.x & 63) >> 5;
     /* scores less the row's maximum so far (the accumulators start at
@@ -807,6 +813,187 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
     finish<D>(A, P, m, lsum, o);
 }
 
+/* a group index as a type: the two key groups' loops use distinct LDS
+   arrays, so the compiler still sees that one buffer's reads never touch
+   the loads in flight into the other */
+template <int N> struct GroupId {
+    static constexpr int value = N;
+};
+
+/*
+ * The f16 kernel for head sizes 72..128 in calls whose 256-row blocks would
+ * leave compute units idle (a prompt of about a thousand tokens, a chunk of
+ * a chunked prefill): 128 rows a workgroup, and the 8 waves are two key
+ * groups of 4 (waves w and w + 4 take the same 32 rows). Group k walks the
+ * k-th half of the block's (or segment's) key tiles of 64 positions - the
+ * first ceil(nt / 2), the rest - with the DMA kernel's loads, swizzle and
+ * tile pass, each group through its own two buffer pairs; group 1's step
+ * past the last tile (nt odd) runs the last tile with every row masked,
+ * which adds nothing. Both groups meet at every tile's barrier. At the end
+ * group 1 puts each row's state (largest score m, sum of weights, values)
+ * into LDS and group 0 combines it with its own - o = 2^(m0 - M) o0 +
+ * 2^(m1 - M) o1, the same for the sum, M = max(m0, m1) - and writes the
+ * output (or the segment's partial). A block's longest chain of tiles is
+ * then half as long as in the DMA kernel, with no partials through memory.
+ */
+template <int D>
+__global__ __launch_bounds__((PCfg<D, true>::W) * 64) void prefill_half_kernel(const PrefillArgs A)
+{
+    using C = PCfg<D, true>;
+    constexpr uint32_t kGW = C::GW, kTile = C::TILE;
+    constexpr uint32_t RB = D * 2;              /* bytes a row */
+    constexpr uint32_t UPR = RB / 16;           /* 16-byte units a row */
+    constexpr uint32_t RPI = 64 / UPR;          /* rows a load instruction */
+    constexpr uint32_t NJ = kTile / (RPI * kGW); /* load instructions a wave */
+    constexpr uint32_t TB = kTile * RB;         /* bytes a tile */
+    constexpr int CT = D / 32;
+    static_assert(NJ * RPI * kGW == kTile, "a tile is whole load rounds");
+    static_assert(TB >= 64 * 16 * CT * 4, "a buffer holds a wave's values");
+    __shared__ __attribute__((aligned(1024))) char sK00[TB];
+    __shared__ __attribute__((aligned(1024))) char sV00[TB];
+    __shared__ __attribute__((aligned(1024))) char sK01[TB];
+    __shared__ __attribute__((aligned(1024))) char sV01[TB];
+    __shared__ __attribute__((aligned(1024))) char sK10[TB];
+    __shared__ __attribute__((aligned(1024))) char sV10[TB];
+    __shared__ __attribute__((aligned(1024))) char sK11[TB];
+    __shared__ __attribute__((aligned(1024))) char sV11[TB];
+    __shared__ float2 sML[kGW][64];
+
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t g = lane >> 5, l32 = lane & 31, l16 = lane & 15;
+    const uint32_t grp = __builtin_amdgcn_readfirstlane(w / kGW);
+    const uint32_t wu = __builtin_amdgcn_readfirstlane(w % kGW);
+    const PBlock P = block_of<D, true>(A);
+    const SeqDesc &sq = *P.sq;
+    const uint32_t hd = A.hd;
+    const bool ring = A.ring != 0;
+    h8 qb[D / 16];
+    load_query<D>(A, P, qb);
+
+    /* the group's tiles: half = ceil(nt / 2) steps from tfirst + grp half */
+    const uint32_t nt = P.tlast - P.tfirst + 1;
+    const uint32_t half = (nt + 1) / 2;
+    const uint32_t gt0 = P.tfirst + grp * half;
+    /* group 1's step past tlast: the last tile, every row masked */
+    PBlock PM = P;
+    PM.rlo = 1;
+    PM.rhi = 0;
+
+    /* loads as in the DMA kernel, over the group's 4 waves */
+    const uint32_t drow = RPI * wu + lane / UPR;
+    uint32_t dcol[NJ];
+#pragma unroll
+    for (int j = 0; j < (int)NJ; j++) {
+        const uint32_t unit = (lane % UPR) ^ swz(drow + RPI * kGW * j);
+        dcol[j] = unit * 8 < hd ? unit * 8 : 0;
+    }
+    const char *const kg = (const char *)sq.k, *const vg = (const char *)sq.v;
+    const uint32_t cap = sq.cap, rbytes = hd * 2;
+    auto fetch = [&](uint32_t tile, char *dk, char *dv) __attribute__((always_inline)) {
+        const uint32_t t0 = tile * kTile;
+        const size_t base = (P.head_row + (ring ? t0 % cap : t0)) * rbytes;
+#pragma unroll
+        for (int j = 0; j < (int)NJ; j++) {
+            uint32_t p = t0 + drow + RPI * kGW * j;
+            p = p < P.lo_all ? P.lo_all : p > P.hi_all ? P.hi_all : p;
+            const uint32_t off = __umul24(p - t0, rbytes) + 2 * dcol[j];
+            const uint32_t at = (wu + kGW * j) * 1024;
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(kg + base + off),
+                (__attribute__((address_space(3))) void *)(dk + at), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(vg + base + off),
+                (__attribute__((address_space(3))) void *)(dv + at), 16, 0, 0);
+        }
+    };
+    uint32_t koff[D / 16];
+#pragma unroll
+    for (int s = 0; s < D / 16; s++)
+        koff[s] = l32 * RB + (((2 * s + g) ^ swz(l16)) * 16);
+    const uint32_t vrow = 4 * g + (l16 >> 2);
+    const uint32_t u0 = 2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1);
+    uint32_t vxo[CT], vyo[CT];
+#pragma unroll
+    for (int c = 0; c < CT; c++) {
+        vxo[c] = vrow * RB + (((4 * c + u0) ^ swz(vrow)) * 16) + (l16 & 1) * 8;
+        vyo[c] = (vrow + 8) * RB + (((4 * c + u0) ^ swz(vrow + 8)) * 16) + (l16 & 1) * 8;
+    }
+
+    float m = -INFINITY, lsum = 0.0f;
+    f16x o[CT];
+#pragma unroll
+    for (int c = 0; c < CT; c++)
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            o[c][i] = 0.0f;
+
+    /* step i of the group from (ck, cv) while step i + 1's tile is loaded
+       into (nk, nv) */
+    auto step = [&](uint32_t i, const char *ck, const char *cv, char *nk, char *nv) __attribute__((always_inline)) {
+        const uint32_t t = gt0 + i;
+        if (i + 1 < half)
+            fetch(t + 1 < P.tlast ? t + 1 : P.tlast, nk, nv);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_pass<D, true, true>(
+            (t < P.tlast ? t : P.tlast) * kTile, t > P.tlast ? PM : P, qb, m, lsum, o,
+            [&](int s, int b) { return *(const h8 *)(ck + 32 * b * RB + koff[s]); },
+            [&](int ks, int c) {
+                const char *base = cv + 16 * ks * RB;
+                const h4 x = lds_read_tr((const _Float16 *)(base + vxo[c]));
+                const h4 y = lds_read_tr((const _Float16 *)(base + vyo[c]));
+                return h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+            });
+        if (i + 1 < half)
+            __syncthreads(); /* the next tiles are in; these are read */
+    };
+    auto run = [&](auto gid) __attribute__((always_inline)) {
+        constexpr int G = decltype(gid)::value;
+        char *const k0 = G ? sK10 : sK00, *const v0 = G ? sV10 : sV00;
+        char *const k1 = G ? sK11 : sK01, *const v1 = G ? sV11 : sV01;
+        fetch(gt0 < P.tlast ? gt0 : P.tlast, k0, v0);
+        __syncthreads();
+        for (uint32_t i = 0;; i += 2) {
+            step(i, k0, v0, k1, v1);
+            if (i + 1 >= half)
+                break;
+            step(i + 1, k1, v1, k0, v0);
+            if (i + 2 >= half)
+                break;
+        }
+    };
+    if (grp == 0)
+        run(GroupId<0>());
+    else
+        run(GroupId<1>());
+
+    /* the halves combined: group 1's state through LDS (the tile buffers,
+       every load landed and every read done at the barrier) */
+    __syncthreads();
+    float *const xo = (float *)(wu == 0 ? sK00 : wu == 1 ? sV00 : wu == 2 ? sK01 : sV01);
+    if (grp == 1) {
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                xo[(16 * c + i) * 64 + lane] = o[c][i];
+        sML[wu][lane] = float2{m, lsum};
+    }
+    __syncthreads();
+    if (grp == 1)
+        return;
+    const float2 ml = sML[wu][lane];
+    const float M = fmaxf(m, ml.x);
+    const float a0 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+    const float a1 = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
+    lsum = lsum * a0 + ml.y * a1;
+#pragma unroll
+    for (int c = 0; c < CT; c++)
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            o[c][i] = o[c][i] * a0 + xo[(16 * c + i) * 64 + lane] * a1;
+    finish<D>(A, P, M, lsum, o);
+}
+
 /*
  * The ordered merge of split rows: thread t of workgroup b takes 4 columns
  * of one row of its sequence (a row is one (token, head)), the pair
@@ -884,6 +1071,14 @@ __global__ __launch_bounds__(kPMergeThreads) void pmerge_kernel(const PrefillArg
 template <int T, int D>
 hipError_t launch_d(const PrefillArgs &a, hipStream_t s)
 {
+    if constexpr (T == kF16 && D == 128) {
+        if (a.halves) {
+            hipLaunchKernelGGL((prefill_half_kernel<D>), dim3(a.n_wg), dim3((PCfg<D, true>::W) * 64), 0, s, a);
+            return hipGetLastError();
+        }
+    }
+    if (a.halves)
+        return hipErrorInvalidValue;
     if constexpr (T == kF16 && (D == 128 || D == 256))
         hipLaunchKernelGGL((prefill_dma_kernel<D>), dim3(a.n_wg), dim3(PCfg<D>::W * 64), 0, s, a);
     else
@@ -913,9 +1108,17 @@ int prefill_supported(int kv, uint32_t hd)
            hd <= 512;
 }
 
-uint32_t prefill_tile(uint32_t hd)
+uint32_t prefill_tile(uint32_t hd, bool halves)
 {
+    if (halves)
+        return PCfg<128, true>::TILE;
     return hd > 256 ? PCfg<512>::TILE : hd > 128 ? PCfg<256>::TILE : PCfg<128>::TILE;
+}
+
+int prefill_halves_supported(int kv, uint32_t hd)
+{
+    /* the DMA kernel's f16 rows at head sizes 72..128 */
+    return kv == kF16 && hd > 64 && hd <= 128;
 }
 
 hipError_t launch_prefill_merge(const PrefillArgs &a, uint32_t n_wg, hipStream_t s)
@@ -924,10 +1127,11 @@ hipError_t launch_prefill_merge(const PrefillArgs &a, uint32_t n_wg, hipStream_t
     return hipGetLastError();
 }
 
-uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd)
+uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd, bool halves)
 {
     /* a workgroup takes PCfg::BLOCK of a KV head's n x group rows */
-    const uint64_t block = hd > 256 ? PCfg<512>::BLOCK
+    const uint64_t block = halves ? PCfg<128, true>::BLOCK
+                         : hd > 256 ? PCfg<512>::BLOCK
                          : hd > 128 ? PCfg<256>::BLOCK : PCfg<128>::BLOCK;
     return (uint32_t)(((uint64_t)n * group + block - 1) / block);
 }

@@ -271,6 +271,76 @@ def test_prefill_split_key_range(name, gpu):
     assert within(err, TOL_F16_ABS, "vs oracle")
 
 
+# (n_head, n_kv, hd, cap, n, pos0, window, ring, span, gate): f16 calls
+# whose DMA-kernel workgroups would leave compute units idle, which take
+# the two-halves kernel (two key groups of 4 waves over 128 rows)
+HALVES = {
+    # 2 key tiles of 64 for the latest block: one a group
+    "tiny_start": (8, 2, 128, 200, 100, 0, 0, False, False, 0),
+    # an odd tile count (19): group 1's last step is masked
+    "odd_tiles_hd96": (8, 2, 96, 1300, 200, 1000, 0, False, False, 0),
+    # 48 tiles for a few blocks: key segments too, merged afterwards
+    "segments": (8, 2, 128, 3100, 64, 3000, 0, False, False, 0),
+    "window_ring": (8, 2, 128, 1024, 150, 2900, 300, True, False, 0),
+    "span_gate": (16, 2, 128, 900, 200, 300, 0, False, True,
+                  janas_amd.GATE_ELEM),
+    "g3_hd80": (6, 2, 80, 700, 333, 200, 0, False, False, janas_amd.GATE_HEAD),
+}
+
+
+@pytest.mark.parametrize("name", sorted(HALVES))
+def test_prefill_halves(name, gpu):
+    """The two-halves kernel against the restatement; the same call twice is
+    bitwise the same."""
+    h, kvh, hd, cap, n, pos0, window, ring, span, gate = HALVES[name]
+    sd = 7700 + sorted(HALVES).index(name) * 10
+    s = dict(k=cache(sd, kvh, cap, hd, np.float16),
+             v=cache(sd + 1, kvh, cap, hd, np.float16),
+             q=normal(sd + 2, n * h * hd).reshape(n, h, hd), pos0=pos0, n=n)
+    if span:
+        p = pos0 + np.arange(n)
+        s["last"] = np.where((p >= pos0 + 40) & (p < pos0 + 90), pos0 + 89,
+                             p).astype(np.uint32)
+    if gate:
+        g_shape = (n, h, hd) if gate == janas_amd.GATE_ELEM else (n, h)
+        s["gate"] = normal(sd + 3, int(np.prod(g_shape))).reshape(g_shape)
+    geom = dict(n_head=h, n_kv=kvh, hd=hd, window=window, ring=ring)
+    with Attention(h, kvh, hd, cap) as a:
+        if window:
+            a.set_window(window)
+        if ring:
+            a.set_ring(True)
+        (out,) = run_prefill(a, [s], gpu, gate_mode=gate)
+        (again,) = run_prefill(a, [s], gpu, gate_mode=gate)
+    assert np.array_equal(out.view(np.int32), again.view(np.int32))
+    err = abs_err(out, oracle(geom, s, gate))
+    print(f"halves {name}: max abs err {err:.2e}")
+    assert within(err, TOL_F16_ABS, "vs oracle")
+
+
+def test_prefill_halves_beside_dma_kernel(gpu):
+    """A launch with sequences for both kernels (a 2048-token chunk fills
+    the GPU with the DMA kernel's segments; the others take the halves):
+    each sequence equals its own call bit for bit."""
+    h, kvh, hd = 8, 2, 128
+    seqs = []
+    for i, (cap, n, pos0) in enumerate([(4096, 2048, 2048), (900, 257, 640),
+                                        (300, 70, 1)]):
+        seqs.append(dict(k=cache(240 + 3 * i, kvh, cap, hd, np.float16),
+                         v=cache(241 + 3 * i, kvh, cap, hd, np.float16),
+                         q=normal(242 + 3 * i, n * h * hd).reshape(n, h, hd),
+                         pos0=pos0, n=n))
+    geom = dict(n_head=h, n_kv=kvh, hd=hd)
+    with Attention(h, kvh, hd, 4096) as a:
+        outs = run_prefill(a, seqs, gpu)
+        for s, out in zip(seqs, outs):
+            (alone,) = run_prefill(a, [s], gpu)
+            assert np.array_equal(out.view(np.int32), alone.view(np.int32))
+            err = abs_err(out, oracle(geom, s))
+            print(f"mixed launch n {s['n']} pos0 {s['pos0']}: max abs err {err:.2e}")
+            assert within(err, TOL_F16_ABS, "vs oracle")
+
+
 def quantized(seed, n_kv, cap, hd, wide):
     """A cache as the engine writes it (model_attn.c:115-145): each row's
     largest magnitude at 127 (32767), its scale max / 127."""
