@@ -328,11 +328,17 @@ __device__ __forceinline__ void load_query(const PrefillArgs &A, const PBlock &P
 struct NoExchange {
     template <class T> __device__ void operator()(T *) const {}
 };
+struct NoLoads {
+    __device__ void operator()(int) const {}
+};
 
-template <int D, bool PIPE, bool HV = false, class KOp, class VOp, class XOp = NoExchange>
+/* lop(s): called at the start of score k-step s (the DMA kernel issues one
+   load instruction of the next tile there) */
+template <int D, bool PIPE, bool HV = false, class KOp, class VOp, class XOp = NoExchange,
+          class LOp = NoLoads>
 __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8 *qb,
                                           float &m, float &lsum, f16x *o,
-                                          KOp kop, VOp vop, XOp xop = XOp())
+                                          KOp kop, VOp vop, XOp xop = XOp(), LOp lop = LOp())
 {
     constexpr int kNPB = PCfg<D, HV>::NPB, kTile = PCfg<D, HV>::TILE;
     constexpr int KS = D / 16 / PCfg<D>::CS, CT = PCfg<D>::OC / 32;
@@ -351,10 +357,12 @@ __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8
        of step s, so the LDS latency hides behind them (32 more registers) */
     if constexpr (!PIPE) {
 #pragma unroll
-        for (int s = 0; s < KS; s++)
+        for (int s = 0; s < KS; s++) {
+            lop(s);
 #pragma unroll
             for (int b = 0; b < kNPB; b++)
                 sacc[b] = mfma(kop(s, b), qb[s], sacc[b]);
+        }
     } else {
     h8 ka[2][kNPB];
 #pragma unroll
@@ -362,6 +370,7 @@ __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8
         ka[0][b] = kop(0, b);
 #pragma unroll
     for (int s = 0; s < KS; s++) {
+        lop(s);
         if (s + 1 < KS)
 #pragma unroll
             for (int b = 0; b < kNPB; b++)
@@ -371,10 +380,13 @@ __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8
             sacc[b] = mfma(ka[s & 1][b], qb[s], sacc[b]);
     }
     /* keep that order: the scheduler would otherwise sink every read to
-       just before its product */
+       just before its product (and the loads of lop to the end) */
+    constexpr bool kLoads = !__is_same(LOp, NoLoads);
     __builtin_amdgcn_sched_group_barrier(0x100, kNPB, 0);
 #pragma unroll
     for (int s = 0; s < KS; s++) {
+        if (kLoads)
+            __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
         if (s + 1 < KS)
             __builtin_amdgcn_sched_group_barrier(0x100, kNPB, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, kNPB, 0);
@@ -757,23 +769,43 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
        multiple of 256 positions): one base a tile, in scalar registers, and
        a 32-bit offset a lane. Rows outside the block's positions read the
        nearest one inside [lo_all, hi_all], which lies in the same tile */
-    auto fetch = [&](uint32_t tile, char *dk, char *dv) {
+    auto tbase = [&](uint32_t tile) -> size_t {
         const uint32_t t0 = tile * kTile;
-        const size_t base = (P.head_row + (ring ? t0 % cap : t0)) * rbytes;
+        return (P.head_row + (ring ? t0 % cap : t0)) * rbytes;
+    };
+    /* the lane's byte offsets in tile `tile` for its NJ load rows */
+    auto offsets = [&](uint32_t tile, uint32_t *off) {
+        const uint32_t t0 = tile * kTile;
 #pragma unroll
         for (int j = 0; j < (int)NJ; j++) {
             uint32_t p = t0 + drow + RPI * kW * j;
             p = p < P.lo_all ? P.lo_all : p > P.hi_all ? P.hi_all : p;
-            const uint32_t off = __umul24(p - t0, rbytes) + 2 * dcol[j];
-            const uint32_t at = (wu + kW * j) * 1024;
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(kg + base + off),
-                (__attribute__((address_space(3))) void *)(dk + at), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(vg + base + off),
-                (__attribute__((address_space(3))) void *)(dv + at), 16, 0, 0);
+            off[j] = __umul24(p - t0, rbytes) + 2 * dcol[j];
         }
     };
+    /* load instruction i of the wave's 2 NJ: rows RPI (w + W (i / 2)) ..,
+       of K (i even) or V (i odd) */
+    auto fetch_one = [&](size_t base, const uint32_t *off, int i, char *dk, char *dv) {
+        const int j = i >> 1;
+        const uint32_t at = (wu + kW * j) * 1024;
+        if (i & 1)
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(vg + base + off[j]),
+                (__attribute__((address_space(3))) void *)(dv + at), 16, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(kg + base + off[j]),
+                (__attribute__((address_space(3))) void *)(dk + at), 16, 0, 0);
+    };
+    auto fetch = [&](uint32_t tile, char *dk, char *dv) {
+        const size_t base = tbase(tile);
+        uint32_t off[NJ];
+        offsets(tile, off);
+#pragma unroll
+        for (int i = 0; i < 2 * (int)NJ; i++)
+            fetch_one(base, off, i, dk, dv);
+    };
+    static_assert(2 * NJ == D / 16, "a load instruction a score k-step");
     /* operand addresses: the lane's score rows are 32 b + l % 32 (row mod
        16 = l % 16), its value rows 16 ks + 4 (l / 32) + (l % 16) / 4 and 8
        further */
@@ -798,13 +830,17 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
         for (int i = 0; i < 16; i++)
             o[c][i] = 0.0f;
 
-    /* tile t from (ck, cv) while t + 1 is loaded into (nk, nv); the
-       scheduling barrier keeps the loads at the top, where they have the
-       whole tile to land */
+    /* tile t from (ck, cv) while t + 1 is loaded into (nk, nv), one load
+       instruction a score k-step: all of a tile's loads at once would hold
+       each wave at the issue until the CU's load path had taken the lot
+       (64 KB at 64 bytes a clock). The block's last tile loads itself again
+       into the other buffer (not read again): a branch per load would cut
+       the score loop's schedule into pieces */
     auto step = [&](uint32_t tile, const char *ck, const char *cv, char *nk, char *nv) {
-        if (tile < P.tlast)
-            fetch(tile + 1, nk, nv);
-        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t nt = tile < P.tlast ? tile + 1 : tile;
+        const size_t nbase = tbase(nt);
+        uint32_t noff[NJ];
+        offsets(nt, noff);
         tile_pass<D, true>(
             tile * kTile, P, qb, m, lsum, o,
             [&](int s, int b) { return *(const h8 *)(ck + 32 * b * RB + koff[s]); },
@@ -813,9 +849,12 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
                 const h4 x = lds_read_tr((const _Float16 *)(base + vxo[c]));
                 const h4 y = lds_read_tr((const _Float16 *)(base + vyo[c]));
                 return h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-            });
+            },
+            NoExchange(), [&](int s) { fetch_one(nbase, noff, s, nk, nv); });
         if (tile < P.tlast)
             __syncthreads(); /* the next tile is in; this one is read */
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* no load into LDS outlives the wave */
     };
 
     fetch(P.tfirst, sK0, sV0);
