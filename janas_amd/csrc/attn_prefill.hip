@@ -16,8 +16,12 @@
  *               a SIMD with 512 registers, and 64-position key tiles; head
  *               size 512: 4 waves as 2 row groups x 2 column halves, 64
  *               rows, 32-position tiles). Row blocks of later tokens (more
- *               keys to see) are dispatched first; consecutive workgroups
- *               share a KV head, so they share an XCD's L2.
+ *               keys to see) are dispatched first; a KV head's blocks go to
+ *               one group of XCDs (they share its L2s), dealt round robin
+ *               among them so that each XCD gets long and short blocks.
+ *               Calls too small to fill the GPU take prefill_half_kernel:
+ *               128 rows a workgroup as two key groups of 4 waves, each
+ *               over half of the key tiles, combined in LDS at the end.
  *   key tiles   128 positions of K and V in LDS, two buffers; the next
  *               tile is loaded while this one is computed. 128 rather than
  *               64 positions: the tile's fixed costs (barriers, the row

@@ -11,9 +11,11 @@
  * the GPU:
  *
  *   split kernel   one workgroup (4 waves of 64, one a SIMD) per (sequence,
- *                  KV head, chunk, tile of 8 query rows); a query row is a
- *                  (token, query head of the KV head's group), so every K/V
- *                  row of the chunk is read once for the whole GQA group.
+ *                  KV head, chunk, one or two tiles of 8 query rows); a
+ *                  query row is a (token, query head of the KV head's
+ *                  group), so every K/V row of the chunk is read once for
+ *                  the whole GQA group (and its operands once for both
+ *                  tiles).
  *                  Wave w streams positions 64 w .. 64 w + 63 in groups of
  *                  16 with two groups in flight, scores each K group as it
  *                  lands, takes a one-shot softmax over its 64 positions and
