@@ -318,6 +318,27 @@ def test_prefill_halves(name, gpu):
     assert within(err, TOL_F16_ABS, "vs oracle")
 
 
+@pytest.mark.parametrize("n_kv,G,n,pos0", [(3, 2, 300, 900), (6, 2, 700, 0),
+                                            (12, 2, 1100, 200)])
+def test_prefill_kv_head_counts(n_kv, G, n, pos0, gpu):
+    """KV head counts whose row blocks are dealt to groups of 8, 4 and 2
+    XCDs (8 / gcd(n_kv, 8)): every workgroup runs once, against the
+    restatement."""
+    h, hd = n_kv * G, 128
+    cap = pos0 + n
+    sd = 7900 + n_kv
+    s = dict(k=cache(sd, n_kv, cap, hd, np.float16),
+             v=cache(sd + 1, n_kv, cap, hd, np.float16),
+             q=normal(sd + 2, n * h * hd).reshape(n, h, hd), pos0=pos0, n=n)
+    geom = dict(n_head=h, n_kv=n_kv, hd=hd)
+    with Attention(h, n_kv, hd, cap) as a:
+        (out,) = run_prefill(a, [s], gpu)
+    err = abs_err(out, oracle(geom, s))
+    print(f"n_kv {n_kv}: max abs err {err:.2e}")
+    assert np.isfinite(out).all()
+    assert within(err, TOL_F16_ABS, "vs oracle")
+
+
 def test_prefill_halves_beside_dma_kernel(gpu):
     """A launch with sequences for both kernels (a 2048-token chunk fills
     the GPU with the DMA kernel's segments; the others take the halves):
