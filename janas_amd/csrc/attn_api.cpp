@@ -49,6 +49,11 @@ struct janas_attn {
        once it is done */
     hipStream_t part_stream;
     hipEvent_t part_ev;
+    /* f16 copies of an int8 / int16 cache's keys and values for long
+       prompts (dequant_bytes each), ordered across streams as the
+       partials */
+    void *dq_k, *dq_v;
+    size_t dq_bytes;
     /* staging of host pointers for janas_attn_run, and the bytes each
        staging buffer holds */
     float *st_q, *st_out;
@@ -413,12 +418,10 @@ bool prefill_halves(const janas_attn *a, int kv, const SeqDesc &d)
 
 /* The sequences in launches of up to kMaxSeqs, those that take the
    two-halves kernel first, then the others. */
-int run_prefill(janas_attn *a, int kv, int gate_mode,
-                const janas_attn_seq *seqs, uint32_t n_seqs, hipStream_t stream,
-                bool fixed = false)
+int run_prefill_launch(janas_attn *a, int kv, int gate_mode,
+                       const janas_attn_seq *seqs, uint32_t n_seqs, hipStream_t stream,
+                       bool fixed)
 {
-    if (!prefill_supported(kv, a->hd))
-        return JANAS_ATTN_ENOTSUP;
     for (int hv = 1; hv >= 0; hv--) {
         for (uint32_t i = 0; i < n_seqs;) {
             PrefillArgs args;
@@ -485,6 +488,114 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
                 if (rc)
                     return rc;
             }
+        }
+    }
+    return JANAS_ATTN_OK;
+}
+
+/* int8 / int16 prompts of at least kDqTokens tokens at head sizes 72..256
+   run over an f16 copy of the rows they see: one pass writes f16(x *
+   scale) - the numbers the register-staged kernel would stage - and the
+   f16 kernels (loads straight into LDS, two halves for short calls) take
+   it from there. The pass is linear in the positions, the prompt's work
+   quadratic. */
+constexpr uint32_t kDqTokens = 256;
+
+int ensure_dq(janas_attn *a, size_t bytes, hipStream_t stream)
+{
+    if (bytes <= a->dq_bytes)
+        return JANAS_ATTN_OK;
+    if (a->dq_k || a->dq_v) {
+        hipError_t e = hipStreamSynchronize(stream);
+        if (e == hipSuccess && a->part_stream && a->part_stream != stream)
+            e = hipStreamSynchronize(a->part_stream);
+        if (e != hipSuccess)
+            return hip_err(e, "synchronize");
+        (void)hipFree(a->dq_k);
+        (void)hipFree(a->dq_v);
+        a->dq_k = a->dq_v = nullptr;
+        a->dq_bytes = 0;
+    }
+    if (hipMalloc(&a->dq_k, bytes) != hipSuccess || hipMalloc(&a->dq_v, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(a->dq_k);
+        (void)hipFree(a->dq_v);
+        a->dq_k = a->dq_v = nullptr;
+        return JANAS_ATTN_ENOMEM;
+    }
+    a->dq_bytes = bytes;
+    return JANAS_ATTN_OK;
+}
+
+/* One int8 / int16 sequence over the f16 copy of its visible rows. */
+int run_prefill_dq(janas_attn *a, int kv, int gate_mode, const janas_attn_seq &s,
+                   hipStream_t stream)
+{
+    SeqDesc d;
+    int rc = describe(a, kv, s, d);
+    if (rc)
+        return rc;
+    const size_t bytes = (size_t)a->n_kv * s.cap * a->hd * sizeof(_Float16);
+    rc = ensure_dq(a, bytes, stream);
+    if (!rc)
+        rc = part_sync(a, stream);
+    if (rc)
+        return rc;
+    DqArgs q;
+    q.k = s.k;
+    q.v = s.v;
+    q.ks = s.ks;
+    q.vs = s.vs;
+    q.k16 = (_Float16 *)a->dq_k;
+    q.v16 = (_Float16 *)a->dq_v;
+    q.n_kv = a->n_kv;
+    q.cap = s.cap;
+    q.hd = a->hd;
+    q.ring = a->ring;
+    /* the chunks the call sees, as the split path counts them */
+    q.p0 = d.c0 * kChunk;
+    q.np = d.end - q.p0;
+    ProfEv *ev = prof_begin(a, 2, stream);
+    hipError_t e = launch_dequant(kv, q, stream);
+    prof_end(ev, stream);
+    if (e != hipSuccess)
+        return hip_err(e, "dequant launch");
+    janas_attn_seq s16 = s;
+    s16.k = a->dq_k;
+    s16.v = a->dq_v;
+    s16.ks = s16.vs = nullptr;
+    return run_prefill_launch(a, kF16, gate_mode, &s16, 1, stream, false);
+}
+
+int run_prefill(janas_attn *a, int kv, int gate_mode,
+                const janas_attn_seq *seqs, uint32_t n_seqs, hipStream_t stream,
+                bool fixed = false)
+{
+    if (!prefill_supported(kv, a->hd))
+        return JANAS_ATTN_ENOTSUP;
+    const bool dq = (kv == kI8 || kv == kI16) && !fixed &&
+                    prefill_supported(kF16, a->hd) && a->hd > 64 && a->hd <= 256;
+    if (!dq)
+        return run_prefill_launch(a, kv, gate_mode, seqs, n_seqs, stream, fixed);
+    /* the long ones one by one over the f16 copy, the others as they are */
+    janas_attn_seq rest[kMaxSeqs];
+    for (uint32_t s0 = 0; s0 < n_seqs; s0 += kMaxSeqs) {
+        const uint32_t m = std::min(kMaxSeqs, n_seqs - s0);
+        uint32_t nr = 0;
+        for (uint32_t i = 0; i < m; i++) {
+            const janas_attn_seq &q = seqs[s0 + i];
+            if (q.n >= kDqTokens && q.k && q.v && q.ks && q.vs) {
+                int rc = run_prefill_dq(a, kv, gate_mode, q, stream);
+                if (rc)
+                    return rc;
+            } else {
+                rest[nr++] = q;
+            }
+        }
+        if (nr) {
+            int rc = run_prefill_launch(a, kv, gate_mode, rest, nr, stream, false);
+            if (rc)
+                return rc;
         }
     }
     return JANAS_ATTN_OK;
@@ -613,6 +724,8 @@ extern "C" void janas_attn_destroy(struct janas_attn *a)
         (void)hipStreamSynchronize(a->part_stream);
     (void)hipFree(a->part_ml);
     (void)hipFree(a->part_acc);
+    (void)hipFree(a->dq_k);
+    (void)hipFree(a->dq_v);
     (void)hipFree(a->st_q);
     (void)hipFree(a->st_out);
     (void)hipFree(a->st_k);

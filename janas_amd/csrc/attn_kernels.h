@@ -89,6 +89,16 @@ struct PrefillArgs {
                               128 rows a workgroup, two key groups */
 };
 
+/* An int8 / int16 cache's rows of positions p0 .. p0 + np - 1 as f16
+   (f16(x * scale)), into a copy laid out as the cache. */
+struct DqArgs {
+    const void *k, *v;
+    const float *ks, *vs;
+    _Float16 *k16, *v16;   /* [n_kv][cap][hd] */
+    uint32_t n_kv, cap, hd, ring;
+    uint32_t p0, np;
+};
+
 /* Rows of a cache write or of the query preparation (attn_cache.hip). */
 struct RowArgs {
     float *k;              /* n x heads x hd: keys, or the queries (in place) */
@@ -178,6 +188,8 @@ uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd, bool halves
 uint32_t prefill_tile(uint32_t hd, bool halves);
 /* 1 when the two-halves kernel takes this element type and head size */
 int prefill_halves_supported(int kv, uint32_t hd);
+/* dequant_kernel (int8 / int16 rows to f16) */
+hipError_t launch_dequant(int kv, const DqArgs &a, hipStream_t s);
 /* the ordered merge of split sequences' segment partials: a thread takes 4
    columns of one row (a row is one (token, head)), a workgroup
    kPMergeThreads of them; a sequence of n tokens takes pmerge_groups of

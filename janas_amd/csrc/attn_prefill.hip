@@ -874,6 +874,35 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
     finish<D>(A, P, m, lsum, o);
 }
 
+/*
+ * The key and value rows of positions p0 .. p0 + np - 1 of every KV head of
+ * an int8 / int16 cache as f16, f16(x * scale) - the numbers
+ * prefill_kernel stages into LDS (PElem::to_f16) - into a copy laid out as
+ * the cache (row kvh cap + p, or p mod cap on a ring), so the f16 kernels
+ * can run over a long prompt of the engine's own format. A thread takes 8
+ * numbers of one row.
+ */
+template <int T>
+__global__ __launch_bounds__(256) void dequant_kernel(const DqArgs A)
+{
+    using E = PElem<T>;
+    const uint32_t upr = A.hd / 8;
+    const uint64_t u = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (u >= (uint64_t)A.n_kv * A.np * upr)
+        return;
+    const uint64_t row = u / upr;
+    const uint32_t cu = (uint32_t)(u - row * upr);
+    const uint32_t kvh = (uint32_t)(row / A.np), p = A.p0 + (uint32_t)(row % A.np);
+    const size_t r = (size_t)kvh * A.cap + (A.ring ? p % A.cap : p);
+    const uint32_t off = cu * 8 * E::EB;
+    const char *kb = (const char *)A.k + r * A.hd * E::EB;
+    const char *vb = (const char *)A.v + r * A.hd * E::EB;
+    const u4 k16 = E::to_f16(E::load(kb, off), A.ks[r]);
+    const u4 v16 = E::to_f16(E::load(vb, off), A.vs[r]);
+    *(u4 *)(A.k16 + r * A.hd + cu * 8) = k16;
+    *(u4 *)(A.v16 + r * A.hd + cu * 8) = v16;
+}
+
 /* a group index as a type: the two key groups' loops use distinct LDS
    arrays, so the compiler still sees that one buffer's reads never touch
    the loads in flight into the other */
@@ -1174,6 +1203,21 @@ uint32_t prefill_tile(uint32_t hd, bool halves)
     if (halves)
         return PCfg<128, true>::TILE;
     return hd > 256 ? PCfg<512>::TILE : hd > 128 ? PCfg<256>::TILE : PCfg<128>::TILE;
+}
+
+hipError_t launch_dequant(int kv, const DqArgs &a, hipStream_t s)
+{
+    const uint64_t n = (uint64_t)a.n_kv * a.np * (a.hd / 8);
+    if (n == 0 || a.hd % 8)
+        return hipErrorInvalidValue;
+    const dim3 grid((uint32_t)((n + 255) / 256));
+    if (kv == kI8)
+        hipLaunchKernelGGL(dequant_kernel<kI8>, grid, dim3(256), 0, s, a);
+    else if (kv == kI16)
+        hipLaunchKernelGGL(dequant_kernel<kI16>, grid, dim3(256), 0, s, a);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
 }
 
 int prefill_halves_supported(int kv, uint32_t hd)

@@ -387,8 +387,9 @@ def quantized(seed, n_kv, cap, hd, wide):
                                        n=300, pos0=400, window=1024)])
 def test_prefill_quantized_cache(gpu, wide, geom):
     """int8 / int16 caches with their scales (the engine's own format) on
-    the MFMA path: rows dequantized into f16 as tiles are staged; the bar is
-    the f16 one."""
+    the MFMA path: rows dequantized into f16 as tiles are staged, or, for
+    prompts of 256 tokens or more at head sizes 72..256, into an f16 copy
+    first; the bar is the f16 one."""
     h, kvh, hd, cap = geom["n_head"], geom["n_kv"], geom["hd"], geom["cap"]
     n, pos0 = geom["n"], geom["pos0"]
     k, ks = quantized(400 + hd, kvh, cap, hd, wide)
@@ -407,12 +408,43 @@ def test_prefill_quantized_cache(gpu, wide, geom):
                             q=to_dev(q, gpu), out=out, cap=cap, n=n,
                             pos0=pos0)], path="prefill")
         torch.cuda.synchronize()
-        assert prefill_launches(a) == 1
+        # the prefill path (and, for long prompts, its f16 copy pass), not
+        # the split path
+        prof = a.prof_read()
+        assert prof["prefill"][0] >= 1 and prof["split"][0] == 0
     ref = orc.run(q, k, v, ks, vs, n_head=h, n_kv=kvh, hd=hd, pos0=pos0,
                   kv=kv, window=geom.get("window", 0),
                   ring=geom.get("ring", False), threads=threads(), block=64)
     err = abs_err(out.cpu().numpy(), ref)
     print(f"{geom} wide={wide}: max abs err {err:.2e}")
+    assert within(err, TOL_F16_ABS, "vs oracle")
+
+
+@pytest.mark.parametrize("wide", [False, True])
+def test_prefill_quantized_long_prompt_f16_copy(gpu, wide):
+    """A long int8 / int16 prompt runs the f16 kernels over an f16 copy of
+    its rows (f16(x * scale), the numbers the register-staged kernel
+    stages): bitwise equal to the allocation-free entry point, which keeps
+    the register-staged kernel, and within the bar of the restatement."""
+    h, kvh, hd, n, pos0 = 32, 8, 128, 2048, 0
+    k, ks = quantized(9100 + wide, kvh, n, hd, wide)
+    v, vs = quantized(9102 + wide, kvh, n, hd, wide)
+    q = normal(9104, n * h * hd).reshape(n, h, hd)
+    kv = janas_amd.KV_I16 if wide else janas_amd.KV_I8
+    d = dict(k=to_dev(k, gpu), v=to_dev(v, gpu), ks=to_dev(ks, gpu),
+             vs=to_dev(vs, gpu), q=to_dev(q, gpu), cap=n, n=n, pos0=pos0)
+    outs = []
+    with Attention(h, kvh, hd, n) as a:
+        for path in ("prefill", "noalloc"):
+            dd = dict(d, out=torch.full(d["q"].shape, float("nan"), device=gpu))
+            a.run_dev(kv, [dd], path=path)
+            torch.cuda.synchronize()
+            outs.append(dd["out"].cpu().numpy())
+    assert np.array_equal(outs[0].view(np.int32), outs[1].view(np.int32))
+    ref = orc.run(q.astype(np.float32), k, v, ks, vs, n_head=h, n_kv=kvh,
+                  hd=hd, pos0=pos0, kv=kv, threads=threads(), block=64)
+    err = abs_err(outs[0], ref)
+    print(f"f16 copy {'int16' if wide else 'int8'}: max abs err {err:.2e}")
     assert within(err, TOL_F16_ABS, "vs oracle")
 
 
