@@ -264,19 +264,23 @@ def bench_decode(torch, jm, w, steps, warmup, kv=None, ncopy=NCOPY,
     return ms, wall, split_ms, merge_ms
 
 
-def bench_prefill(torch, jm, w, steps, warmup):
+def bench_prefill(torch, jm, w, steps, warmup, kv=None):
     """One causal prefill call of the whole prompt, launches back to back on
-    a stream of its own, HIP events around them on that stream."""
+    a stream of its own, HIP events around them on that stream. kv: the
+    cache's element type (f16 by default; int8 / int16 with w's scales)."""
     dev = torch.device("cuda:0")
     k = torch.from_numpy(w["k"]).to(dev)
     v = torch.from_numpy(w["v"]).to(dev)
     q = torch.from_numpy(w["q"]).to(dev)
+    kz = torch.from_numpy(w["ks"]).to(dev) if "ks" in w else None
+    vz = torch.from_numpy(w["vs"]).to(dev) if "vs" in w else None
     out = torch.empty_like(q)
     stream = torch.cuda.Stream()
     assert stream.cuda_stream != 0
     with jm.Attention(w["h"], w["kvh"], w["hd"], w["L"]) as a:
-        call = a.prepare(jm.KV_F16, [dict(k=k, v=v, q=q, out=out, cap=w["L"],
-                                          n=w["L"], pos0=0)],
+        call = a.prepare(jm.KV_F16 if kv is None else kv,
+                         [dict(k=k, v=v, ks=kz, vs=vz, q=q, out=out,
+                               cap=w["L"], n=w["L"], pos0=0)],
                          stream=stream.cuda_stream, path="prefill")
         for _ in range(warmup):
             call()
@@ -453,12 +457,13 @@ def wide_leg(torch, jm, steps, warmup):
     }
 
 
-def int_decode_leg(torch, jm, steps, warmup):
-    """Config 4's decode over int8 and int16 caches: the step (split +
-    merge), with the split kernel's own time and HBM rate. Bytes: keys,
-    values and their scales once. int8 twice: the FLOAT scores way, and the
-    INT16 way (which AUTO resolves to at this context, as the
-    reference's)."""
+def int_leg(torch, jm, steps, warmup, prefill_steps=5):
+    """The engine's own cache formats. Config 4's decode over int8 and int16
+    caches: the step (split + merge), with the split kernel's own time and
+    HBM rate; bytes: keys, values and their scales once. int8 twice: the
+    FLOAT scores way, and the INT16 way (which AUTO resolves to at this
+    context, as the reference's). Then the 8k prefill over the same prompt's
+    rows quantized to int8 and to int16."""
     res = {}
     for name, dtype, kv, ncopy, scores in (
             ("4-int8", np.int8, jm.KV_I8, 8, jm.FLOAT),
@@ -480,6 +485,22 @@ def int_decode_leg(torch, jm, steps, warmup):
                      "split_us": round(split_ms * 1e3, 3),
                      "split_frac": round(b / (split_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "merge_us": round(merge_ms * 1e3, 3)}
+    w = prefill_workload()
+    fl = prefill_flops(w["hd"], w["h"], 0, w["L"])
+    for name, dtype, kv in (("8k-prefill-int8", np.int8, jm.KV_I8),
+                            ("8k-prefill-int16", np.int16, jm.KV_I16)):
+        k, ks = quantized(w["k"], dtype)
+        v, vs = quantized(w["v"], dtype)
+        ms = bench_prefill(torch, jm, dict(w, k=k, v=v, ks=ks, vs=vs),
+                           prefill_steps, 2, kv=kv)
+        tf = fl / (ms * 1e-3) / 1e12
+        res[name] = {"workload": "causal prefill, 32 Q / 8 KV heads, head_dim "
+                                 f"128, 8192 tokens, {np.dtype(dtype).name} K/V "
+                                 "with per-row scales (the f16 prompt's rows "
+                                 "quantized), f32 q",
+                     "ms": round(ms, 4), "value": round(tf, 2),
+                     "unit": "TFLOP/s", "flops": fl, "bound": "mfma",
+                     "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
     return res
 
 
@@ -515,7 +536,7 @@ def main():
         print(json.dumps(configs_leg(torch, jm)), flush=True)
         return
     if args.only == "int":
-        print(json.dumps(int_decode_leg(torch, jm, args.steps, args.warmup)),
+        print(json.dumps(int_leg(torch, jm, args.steps, args.warmup)),
               flush=True)
         return
     if args.only == "prefill":
@@ -586,7 +607,7 @@ def main():
     line["wide"] = wide_leg(torch, jm, max(1, args.steps // 4),
                             min(args.warmup, 20))
     line["configs"] = configs_leg(torch, jm)
-    line["configs"].update(int_decode_leg(torch, jm, max(1, args.steps // 2),
+    line["configs"].update(int_leg(torch, jm, max(1, args.steps // 2),
                                           min(args.warmup, 20)))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_decode_baseline(w)
