@@ -585,7 +585,11 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
         for (uint32_t i = 0; i < m; i++) {
             const janas_attn_seq &q = seqs[s0 + i];
             if (q.n >= kDqTokens && q.k && q.v && q.ks && q.vs) {
+                /* no memory for the copy: the register-staged kernel,
+                   which needs none */
                 int rc = run_prefill_dq(a, kv, gate_mode, q, stream);
+                if (rc == JANAS_ATTN_ENOMEM)
+                    rc = run_prefill_launch(a, kv, gate_mode, &q, 1, stream, false);
                 if (rc)
                     return rc;
             } else {
