@@ -49,6 +49,13 @@
 #include "attn_elem.h"
 #include "attn_q8k.h"
 
+/* A token's result must not depend on the instance its call takes (one or
+   two row tiles, one sequence or several, 32, 128 or 256 merge columns):
+   each computes a row with the same operations, but left free the compiler
+   fuses a different product of a sum like a b + c d into a multiply-add in
+   each instance. So nothing is fused here but what is written as fmaf. */
+#pragma clang fp contract(off)
+
 namespace janas {
 namespace {
 

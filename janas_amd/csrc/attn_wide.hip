@@ -46,6 +46,11 @@
 
 #include "attn_elem.h"
 
+/* One instance or another (one sequence, several), a row is computed with
+   the same operations: nothing is fused into multiply-adds but what is
+   written as fmaf, so the compiler cannot fuse differently per instance. */
+#pragma clang fp contract(off)
+
 namespace janas {
 namespace {
 
