@@ -141,7 +141,9 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     const uint32_t rows_here = R - r0 < kRows ? R - r0 : kRows;
     const uint32_t jf = r0 / G, jl = (r0 + rows_here - 1) / G;
     const uint32_t lo_all = row_lo(A, sq.pos0 + jf);
-    const uint32_t hi_all = sq.last ? sq.last[jl] : sq.pos0 + jl;
+    /* a last[] past the call's end counts as its end */
+    uint32_t hi_all = sq.last ? sq.last[jl] : sq.pos0 + jl;
+    hi_all = hi_all < sq.end - 1 ? hi_all : sq.end - 1;
     if (t0 > hi_all || t0 + kChunk <= lo_all)
         return;
     const uint32_t p0w = t0 + w * kWPos;
