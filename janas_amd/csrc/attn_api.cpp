@@ -285,8 +285,66 @@ void prof_end(ProfEv *ev, hipStream_t stream)
         (void)hipEventRecord(ev->b, stream);
 }
 
+/* JANAS_ATTN_SKIPSTAT=1 (attention.c:841-869, :1320-1325): how many
+   chunks a row could have skipped, had it known in advance which ones
+   weigh nothing - their largest score more than 8, 16 or 32 below the
+   row's - printed when the program ends, over all rows and over those past
+   16384 positions. Read at the first janas_attn_create of the process;
+   counted by the merge of the split path (decode, verify, blocks), on the
+   device, into counters each device holds from that create on. The
+   prefill kernels keep no chunk partials and are not counted. */
+constexpr int kSkipDevs = 64;
+int g_skip = -1;
+unsigned long long *g_skip_dev[kSkipDevs];
+
+void skip_report()
+{
+    static const char *what[2] = {"all rows", "rows past 16384"};
+    unsigned long long t[8] = {0};
+    for (int d = 0; d < kSkipDevs; d++) {
+        unsigned long long h[8];
+        if (!g_skip_dev[d] || hipSetDevice(d) != hipSuccess ||
+            hipMemcpy(h, g_skip_dev[d], sizeof h, hipMemcpyDeviceToHost) != hipSuccess)
+            continue;
+        for (int i = 0; i < 8; i++)
+            t[i] += h[i];
+    }
+    for (int w = 0; w < 2; w++) {
+        const unsigned long long n = t[w];
+        if (!n)
+            continue;
+        fprintf(stderr,
+                "attention skip ceiling, %s: %llu chunks; below max-8 "
+                "%.1f%%, max-16 %.1f%%, max-32 %.1f%%\n",
+                what[w], n, 100.0 * t[2 + 3 * w] / n, 100.0 * t[3 + 3 * w] / n,
+                100.0 * t[4 + 3 * w] / n);
+    }
+}
+
+/* the counters of device dev, allocated at a create on it (null: off, or
+   the allocation failed, which leaves the statistic off there) */
+void skip_init(int dev)
+{
+    if (g_skip < 0) {
+        const char *e = getenv("JANAS_ATTN_SKIPSTAT");
+        g_skip = e && atoi(e) > 0;
+        if (g_skip)
+            atexit(skip_report);
+    }
+    if (!g_skip || dev < 0 || dev >= kSkipDevs || g_skip_dev[dev])
+        return;
+    unsigned long long *p = nullptr;
+    if (hipMalloc(&p, 8 * sizeof *p) != hipSuccess || hipMemset(p, 0, 8 * sizeof *p) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(p);
+        return;
+    }
+    g_skip_dev[dev] = p;
+}
+
 int fill_args(const janas_attn *a, int kv, SplitArgs &args, int gate_mode, const Parts &p)
 {
+    args.skip = g_skip > 0 && a->dev >= 0 && a->dev < kSkipDevs ? g_skip_dev[a->dev] : nullptr;
     /* the INT16 way exists over int8 caches (attention.c:692, :1061-1066) */
     args.int16 = kv == kI8 && a->scores == JANAS_ATTN_INT16;
     args.part_ml = p.ml;
@@ -695,6 +753,7 @@ extern "C" struct janas_attn *janas_attn_create(uint32_t n_head,
     /* the allocation-free entry point's partials on this device (a failure
        only disables that entry point) */
     (void)scratch_init(dev);
+    skip_init(dev);
     /* a blocking stream: the calls that run on it (janas_attn_run, and
        Part 2 with a NULL stream) are ordered after work the caller queued
        on the legacy default stream - row writes, copies - and before what

@@ -72,6 +72,11 @@ struct SplitArgs {
     int gate_mode;
     int int16;             /* the reference's INT16 scores (int8 caches,
                               hd a multiple of 16) */
+    /* JANAS_ATTN_SKIPSTAT (attention.c:841-869, :883-898): counters of
+       the chunks a (token, head) merged - n[2], then below[2][3] (more than
+       8, 16, 32 below the row's largest score), [0] all rows, [1] rows past
+       16384 positions - or null when off */
+    unsigned long long *skip;
 };
 
 /* The causal MFMA pass over whole prompts (prefill, chunked prefill). */

@@ -892,6 +892,29 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
             wk[k] = sM[k][cl] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sM[k][cl] - mx);
             wl[k] = wk[k] * sL[k][cl];
         }
+        if (A.skip && col == 0) {
+            /* JANAS_ATTN_SKIPSTAT: how many of the row's chunks lie more
+               than 8, 16 or 32 (natural units; m is in powers of two) below
+               its largest score, as merge_one counts them
+               (attention.c:883-898): from the call's first chunk, so the
+               chunks before the token's own window count as below, and n
+               counts from chunk 0 */
+            unsigned long long k[3] = {clo - sq.c0, clo - sq.c0, clo - sq.c0};
+            for (uint32_t i = 0; i < nc; i++) {
+                const float mi = A.part_ml[(base + (uint64_t)i * R) * 2];
+                k[0] += mi < mx - 8.0f * kLog2e;
+                k[1] += mi < mx - 16.0f * kLog2e;
+                k[2] += mi < mx - 32.0f * kLog2e;
+            }
+            for (int wq = 0; wq < 2; wq++) {
+                if (wq == 1 && pos < 16384)
+                    break;
+                atomicAdd(&A.skip[wq], (unsigned long long)(hi / kChunk + 1));
+#pragma unroll
+                for (int t = 0; t < 3; t++)
+                    atomicAdd(&A.skip[2 + 3 * wq + t], k[t]);
+            }
+        }
         const float sum = ((wl[0] + wl[1]) + (wl[2] + wl[3])) + ((wl[4] + wl[5]) + (wl[6] + wl[7]));
         const float inv = 1.0f / sum;
         float4 o[NV];
