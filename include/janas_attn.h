@@ -53,9 +53,13 @@ extern "C" {
    reference's bit for bit. janas_attn_create resolves the asked way as the
    reference does (attention.c:960-982, the JANAS_ATTN environment variable
    first): AUTO is INT16 past 16384 positions; head_dim not a multiple of
-   16, or janas_attn_set_kv16(a, 1), makes it FLOAT. The reference's
-   calibration of AUTO (timing both ways on the host CPU, attention.c:1080-
-   1262) has no counterpart: the resolved way holds for every call. */
+   16, or janas_attn_set_kv16(a, 1), makes it FLOAT. Then, as the
+   reference's janas_attn_run does (attention.c:1183-1262), AUTO over an
+   int8 cache measures both ways once, on the device, at its first call,
+   and each call takes INT16 from the position measured on (per one token
+   and per block): janas_attn_scores_mode reports the last call's way. A
+   Part 2 call of one sequence on the split path chooses the same way; one
+   captured into a graph before any measurement keeps the last one. */
 enum janas_attn_scores {
     JANAS_ATTN_AUTO = 0,
     JANAS_ATTN_FLOAT = 1,

@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include <hip/hip_runtime.h>
@@ -34,6 +35,10 @@ struct janas_attn {
     uint32_t n_head, n_kv, hd, n_ctx, group;
     int scores;           /* JANAS_ATTN_FLOAT or _INT16, as resolved */
     int scores_auto;
+    /* AUTO over int8 caches: INT16 from position from16[n > 1] on,
+       measured on the device at the first call (calibrate) */
+    uint32_t from16[2];
+    int calibrated;
     float scale;
     uint32_t window;
     int kv16, ring;
@@ -430,6 +435,175 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
         }
     }
     return JANAS_ATTN_OK;
+}
+
+/*
+ * AUTO's way, measured (attn_calibrate, attention.c:1183-1262): over a
+ * made-up int8 cache of this instance's geometry (as far as 65536 + 64
+ * positions, a ring its whole capacity), one token at positions 1024,
+ * 2048, ... up to 65536 and a 64-token block up to 16384 are timed both
+ * ways on the device (the faster of three calls each, HIP events on the
+ * instance's stream); INT16 is taken from the first position from which it
+ * wins at every longer one. The reference keeps its measurements in a file
+ * under its cache directory; here they are kept for the process, by device
+ * and geometry. On gfx950 INT16 costs 5-8 % more than FLOAT at every
+ * length, so AUTO measures to FLOAT.
+ */
+struct Calib {
+    int dev, ring;
+    uint32_t n_head, n_kv, hd, window, n_ctx;
+    uint32_t from16[2];
+};
+std::mutex g_calib_mu;
+std::vector<Calib> *g_calib;
+
+bool calib_same(const Calib &c, const janas_attn *a)
+{
+    return c.dev == a->dev && c.ring == a->ring && c.n_head == a->n_head && c.n_kv == a->n_kv &&
+           c.hd == a->hd && c.window == a->window && c.n_ctx == a->n_ctx;
+}
+
+/* milliseconds of the faster of three calls of this way, or -1 */
+float time_way(janas_attn *a, int way, const janas_attn_seq &s, hipEvent_t e0, hipEvent_t e1)
+{
+    float best = 1e30f;
+    a->scores = way;
+    for (int r = 0; r < 3; r++) {
+        if (hipEventRecord(e0, a->stream) != hipSuccess)
+            return -1.0f;
+        const int rc = run_split(a, kI8, kGateNone, &s, 1, a->stream);
+        if (rc || hipEventRecord(e1, a->stream) != hipSuccess ||
+            hipEventSynchronize(e1) != hipSuccess)
+            return -1.0f;
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+            return -1.0f;
+        best = std::min(best, ms);
+    }
+    return best;
+}
+
+void calibrate(janas_attn *a)
+{
+    a->calibrated = 1;
+    a->from16[0] = a->from16[1] = UINT32_MAX;
+    {
+        std::lock_guard<std::mutex> lk(g_calib_mu);
+        if (g_calib)
+            for (const Calib &c : *g_calib)
+                if (calib_same(c, a)) {
+                    a->from16[0] = c.from16[0];
+                    a->from16[1] = c.from16[1];
+                    return;
+                }
+    }
+    const uint32_t nb = JANAS_ATTN_MAX_BLOCK < 64 ? JANAS_ATTN_MAX_BLOCK : 64;
+    const uint32_t top = !a->ring && a->n_ctx > 65536 + nb ? 65536 + nb : a->n_ctx;
+    const size_t cells = (size_t)a->n_kv * top;
+    const size_t qn = (size_t)nb * a->n_head * a->hd;
+    void *k = nullptr, *v = nullptr, *ks = nullptr, *vs = nullptr, *q = nullptr, *out = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    const int keep = a->scores;
+    bool ok = hipMalloc(&k, cells * a->hd) == hipSuccess &&
+              hipMalloc(&v, cells * a->hd) == hipSuccess &&
+              hipMalloc(&ks, cells * sizeof(float)) == hipSuccess &&
+              hipMalloc(&vs, cells * sizeof(float)) == hipSuccess &&
+              hipMalloc(&q, qn * sizeof(float)) == hipSuccess &&
+              hipMalloc(&out, qn * sizeof(float)) == hipSuccess &&
+              hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess;
+    if (ok) {
+        /* made-up numbers: the time of a way does not hang on them */
+        const float sc = 0.01f, qv = 0.5f;
+        uint32_t scb, qb;
+        memcpy(&scb, &sc, 4);
+        memcpy(&qb, &qv, 4);
+        ok = hipMemsetAsync(k, 0x35, cells * a->hd, a->stream) == hipSuccess &&
+             hipMemsetAsync(v, 0xC9, cells * a->hd, a->stream) == hipSuccess &&
+             hipMemsetD32Async((hipDeviceptr_t)ks, (int)scb, cells, a->stream) == hipSuccess &&
+             hipMemsetD32Async((hipDeviceptr_t)vs, (int)scb, cells, a->stream) == hipSuccess &&
+             hipMemsetD32Async((hipDeviceptr_t)q, (int)qb, qn, a->stream) == hipSuccess;
+    }
+    for (int c = 0; ok && c < 2; c++) {
+        const uint32_t n = c ? nb : 1, limit = c ? 16384 : 65536;
+        uint32_t from = UINT32_MAX;
+        for (uint32_t p = 1024; ok && p + n <= top && p <= limit; p *= 2) {
+            janas_attn_seq s;
+            memset(&s, 0, sizeof s);
+            s.k = k;
+            s.v = v;
+            s.ks = (const float *)ks;
+            s.vs = (const float *)vs;
+            s.q = (const float *)q;
+            s.out = (float *)out;
+            s.cap = top;
+            s.n = n;
+            s.pos0 = p;
+            const float tf = time_way(a, JANAS_ATTN_FLOAT, s, e0, e1);
+            const float ti = time_way(a, JANAS_ATTN_INT16, s, e0, e1);
+            if (tf < 0.0f || ti < 0.0f) {
+                ok = false;
+                break;
+            }
+            if (ti < tf) {
+                if (from == UINT32_MAX)
+                    from = p;
+            } else {
+                from = UINT32_MAX; /* it must win at every longer one */
+            }
+        }
+        if (ok)
+            a->from16[c] = from;
+    }
+    if (!ok) {
+        /* a failed measurement leaves FLOAT, and no trace in the status */
+        a->from16[0] = a->from16[1] = UINT32_MAX;
+        (void)hipGetLastError();
+    }
+    (void)hipStreamSynchronize(a->stream);
+    for (void *p : {k, v, ks, vs, q, out})
+        (void)hipFree(p);
+    if (e0)
+        (void)hipEventDestroy(e0);
+    if (e1)
+        (void)hipEventDestroy(e1);
+    a->scores = keep;
+    if (!ok)
+        return;
+    std::lock_guard<std::mutex> lk(g_calib_mu);
+    if (!g_calib)
+        g_calib = new std::vector<Calib>();
+    g_calib->push_back(Calib{a->dev, a->ring, a->n_head, a->n_kv, a->hd, a->window, a->n_ctx,
+                             {a->from16[0], a->from16[1]}});
+}
+
+/* The engine's choice for a call of n tokens at pos0 (janas_attn_run,
+   attention.c:1255-1260): under AUTO over an int8 cache, measured once */
+void choose_way(janas_attn *a, int kv, uint32_t n, uint32_t pos0)
+{
+    if (!a->scores_auto || a->kv16 || kv != kI8 || a->hd % 16)
+        return;
+    if (!a->calibrated)
+        calibrate(a);
+    a->scores = pos0 >= a->from16[n > 1] ? JANAS_ATTN_INT16 : JANAS_ATTN_FLOAT;
+}
+
+/* The same choice for a Part 2 call of one sequence on the split path,
+   unless the stream is being captured into a graph (the first call's
+   measurement allocates and synchronizes; a captured call keeps the way
+   last resolved) */
+void choose_way_dev(janas_attn *a, int kv, const janas_attn_seq *seqs, uint32_t n_seqs,
+                    hipStream_t st)
+{
+    if (n_seqs != 1 || seqs[0].n > JANAS_ATTN_MAX_BLOCK)
+        return;
+    if (!a->calibrated) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+            (void)hipGetLastError();
+            return;
+        }
+    }
+    choose_way(a, kv, seqs[0].n, seqs[0].pos0);
 }
 
 /* Key segments for a prefill sequence whose row blocks alone would leave
@@ -1023,6 +1197,7 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
         s.last = a->st_last;
         s.last_max = last[n - 1];
     }
+    choose_way(a, kv, n, pos0);
     rc = run_split(a, kv, kGateNone, &s, 1, a->stream);
     if (rc) {
         (void)hipStreamSynchronize(a->stream);
@@ -1071,6 +1246,7 @@ extern "C" int janas_attn_run_dev_split(struct janas_attn *a, int kv_type,
     if (rc)
         return rc;
     hipStream_t st = stream ? (hipStream_t)stream : a->stream;
+    choose_way_dev(a, kv_type, seqs, n_seqs, st);
     rc = run_split(a, kv_type, gate_mode, seqs, n_seqs, st);
     return note(a, rc);
 }
@@ -1099,6 +1275,8 @@ int run_dev(janas_attn *a, int kv_type, int gate_mode, const janas_attn_seq *seq
     if (rc)
         return rc;
     hipStream_t st = stream ? (hipStream_t)stream : a->stream;
+    if (!fixed)
+        choose_way_dev(a, kv_type, seqs, n_seqs, st);
     /* blocks of up to JANAS_ATTN_MAX_BLOCK tokens keep the split-KV
        chunking of janas_attn_run; longer prompts take the prefill tiles */
     bool any_long = false;

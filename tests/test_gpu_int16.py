@@ -12,9 +12,11 @@ quantized per (chunk, token, head) and exact integer value sums
   merge's float rounding differs - and against the double-precision
   closed form at the reference's INT16 bar (test_attention.c:143-148);
 * a block equals its tokens one by one, bit for bit;
-* config 4's geometry at 32k positions (AUTO resolves to INT16 there), the
-  wide kernel's head sizes, windows, rings and last[], against the
-  restatement's INT16 way.
+* config 4's geometry at 32k positions, the wide kernel's head sizes,
+  windows, rings and last[], against the restatement's INT16 way;
+* AUTO: resolved at create as scores_choice does, then per call by the
+  positions measured on the device at the first call (attn_calibrate,
+  attention.c:1183-1262): a call's output is the chosen way's, bit for bit.
 """
 import numpy as np
 import pytest
@@ -162,15 +164,14 @@ def int8_cache(seed, n_kv, cap, hd):
 
 
 def test_int16_config4_geometry_at_32k(gpu):
-    """16/2/256 over 32768 int8 positions: AUTO resolves to INT16 at this
-    size; one decode token and a 5-token block against the restatement's
-    INT16 way."""
+    """16/2/256 over 32768 int8 positions under INT16: one decode token and
+    a 5-token block against the restatement's INT16 way."""
     h, kvh, hd, L = 16, 2, 256, 32768
     k, ks = int8_cache(501, kvh, L, hd)
     v, vs = int8_cache(502, kvh, L, hd)
     q = normal(503, 5 * h * hd).reshape(5, h, hd)
     kd, vd, ksd, vsd = (to_dev(x, gpu) for x in (k, v, ks, vs))
-    with Attention(h, kvh, hd, L) as a:
+    with Attention(h, kvh, hd, L, 1, janas_amd.INT16) as a:
         assert a.scores_mode() == janas_amd.INT16
         a.set_scale(1.0 / 16.0)
         for n in (1, 5):
@@ -305,3 +306,46 @@ def test_int16_noalloc_and_q8k(gpu):
                       kv=orc.KV_I8, int16=True, threads=threads())
         bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
         assert within(abs_err(o, ref), bar, f"int16 noalloc q8k n={n}")
+
+
+def test_auto_measured_way(gpu, monkeypatch):
+    """AUTO over an int8 cache: INT16 at create past 16384 positions (the
+    reference's scores_choice), then per call the way measured on the device
+    at the first call - janas_attn_scores_mode reports it, and the output is
+    that way's bit for bit, through the drop-in and through Part 2. The same
+    instance geometry later reuses the measurement. Under set_kv16 AUTO
+    stays FLOAT without measuring."""
+    monkeypatch.delenv("JANAS_ATTN", raising=False)
+    h, kvh, hd, L = 16, 2, 256, 20000
+    k, ks = int8_cache(601, kvh, L, hd)
+    v, vs = int8_cache(602, kvh, L, hd)
+    q = normal(603, 4 * h * hd).reshape(4, h, hd)
+    kd, vd, ksd, vsd, qd = (to_dev(x, gpu) for x in (k, v, ks, vs, q))
+    for n, pos0 in ((1, L - 1), (4, 17000), (1, 1500)):
+        outs = {}
+        for scores in (janas_amd.AUTO, janas_amd.FLOAT, janas_amd.INT16):
+            out = torch.zeros((n, h, hd), dtype=torch.float32, device=gpu)
+            with Attention(h, kvh, hd, L, 1, scores) as a:
+                if scores == janas_amd.AUTO:
+                    assert a.scores_mode() == janas_amd.INT16
+                a.run(qd[:n], kd, ksd, vd, vsd, n, pos0, out)
+                torch.cuda.synchronize()
+                outs[scores] = (a.scores_mode(), out.cpu().numpy())
+        way, got = outs[janas_amd.AUTO]
+        assert way in (janas_amd.FLOAT, janas_amd.INT16)
+        print(f"n={n} pos0={pos0}: AUTO measured "
+              f"{'INT16' if way == janas_amd.INT16 else 'FLOAT'}")
+        assert np.array_equal(got.view(np.uint32), outs[way][1].view(np.uint32))
+        # Part 2, one sequence on the split path: the same choice
+        out = torch.zeros((n, h, hd), dtype=torch.float32, device=gpu)
+        with Attention(h, kvh, hd, L, 1, janas_amd.AUTO) as a:
+            a.run_dev(janas_amd.KV_I8, [dict(k=kd, v=vd, ks=ksd, vs=vsd,
+                                              q=qd[:n], out=out, cap=L, n=n,
+                                              pos0=pos0)])
+            torch.cuda.synchronize()
+            assert a.scores_mode() == way
+        assert np.array_equal(out.cpu().numpy().view(np.uint32),
+                              got.view(np.uint32))
+    with Attention(h, kvh, 128, L, 1, janas_amd.AUTO) as a:
+        a.set_kv16(True)
+        assert a.scores_mode() == janas_amd.FLOAT
