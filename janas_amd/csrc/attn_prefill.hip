@@ -720,6 +720,28 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_kernel(const PrefillA
  * the compiler then sees that reads of one pair never touch the loads in
  * flight into the other, and waits for those only at the tile's barrier.
  */
+/*
+ * One 16-byte-a-lane load from global memory straight into LDS
+ * (global_load_lds_dwordx4: lane l's 16 bytes at gbase + voff land at LDS
+ * address m0 + 16 l), written out rather than through the builtin. The
+ * compiler's wait counting takes a load into LDS as outstanding work of the
+ * LDS counter too, so with one in flight it makes every LDS operand wait
+ * drain all reads (lgkmcnt(0)), and the operand reads issued a k-step
+ * ahead no longer overlap the products. The hardware counts these loads in
+ * the vector-memory counter only (measured: after one such load and one LDS
+ * read, lgkmcnt(0) returns with the read while vmcnt(0) waits for the load),
+ * so they are kept out of the compiler's sight, and every wave waits for its
+ * own (s_waitcnt vmcnt(0)) before the barrier that publishes the tile. M0 is
+ * set here; nothing else in these kernels reads it (the compiler sets it
+ * before each use of its own).
+ */
+__device__ __forceinline__ void dma16(const char *gbase, uint32_t voff, char *lds)
+{
+    const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :: "s"(__builtin_amdgcn_readfirstlane(m0)), "v"(voff), "s"(gbase));
+}
+
 __device__ __forceinline__ uint32_t swz(uint32_t r)
 {
     r &= 15;
@@ -793,13 +815,9 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
         const int j = i >> 1;
         const uint32_t at = (wu + kW * j) * 1024;
         if (i & 1)
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(vg + base + off[j]),
-                (__attribute__((address_space(3))) void *)(dv + at), 16, 0, 0);
+            dma16(vg + base, off[j], dv + at);
         else
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(kg + base + off[j]),
-                (__attribute__((address_space(3))) void *)(dk + at), 16, 0, 0);
+            dma16(kg + base, off[j], dk + at);
     };
     auto fetch = [&](uint32_t tile, char *dk, char *dv) {
         const size_t base = tbase(tile);
@@ -855,13 +873,15 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
                 return h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
             },
             NoExchange(), [&](int s) { fetch_one(nbase, noff, s, nk, nv); });
+        /* the wave's loads of the next tile are in (the last tile's, of
+           itself again: no load into LDS outlives the wave) */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (tile < P.tlast)
-            __syncthreads(); /* the next tile is in; this one is read */
-        else
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* no load into LDS outlives the wave */
+            __syncthreads(); /* the whole next tile is in; this one is read */
     };
 
     fetch(P.tfirst, sK0, sV0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     for (uint32_t tile = P.tfirst;; tile += 2) {
         step(tile, sK0, sV0, sK1, sV1);
@@ -988,12 +1008,8 @@ __global__ __launch_bounds__((PCfg<D, true>::W) * 64) void prefill_half_kernel(c
             p = p < P.lo_all ? P.lo_all : p > P.hi_all ? P.hi_all : p;
             const uint32_t off = __umul24(p - t0, rbytes) + 2 * dcol[j];
             const uint32_t at = (wu + kGW * j) * 1024;
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(kg + base + off),
-                (__attribute__((address_space(3))) void *)(dk + at), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(vg + base + off),
-                (__attribute__((address_space(3))) void *)(dv + at), 16, 0, 0);
+            dma16(kg + base, off, dk + at);
+            dma16(vg + base, off, dv + at);
         }
     };
     uint32_t koff[D / 16];
@@ -1033,6 +1049,8 @@ __global__ __launch_bounds__((PCfg<D, true>::W) * 64) void prefill_half_kernel(c
                 const h4 y = lds_read_tr((const _Float16 *)(base + vyo[c]));
                 return h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
             });
+        /* the wave's loads of the next tile are in (dma16) */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (i + 1 < half)
             __syncthreads(); /* the next tiles are in; these are read */
     };
@@ -1041,6 +1059,7 @@ __global__ __launch_bounds__((PCfg<D, true>::W) * 64) void prefill_half_kernel(c
         char *const k0 = G ? sK10 : sK00, *const v0 = G ? sV10 : sV00;
         char *const k1 = G ? sK11 : sK01, *const v1 = G ? sV11 : sV01;
         fetch(gt0 < P.tlast ? gt0 : P.tlast, k0, v0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         for (uint32_t i = 0;; i += 2) {
             step(i, k0, v0, k1, v1);
@@ -1058,6 +1077,7 @@ __global__ __launch_bounds__((PCfg<D, true>::W) * 64) void prefill_half_kernel(c
 
     /* the halves combined: group 1's state through LDS (the tile buffers,
        every load landed and every read done at the barrier) */
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     float *const xo = (float *)(wu == 0 ? sK00 : wu == 1 ? sV00 : wu == 2 ? sK01 : sV01);
     if (grp == 1) {
