@@ -706,19 +706,22 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_kernel(const PrefillA
  *
  * A tile is 128 rows of 256 bytes (head size 128; 8 waves) or 64 rows of
  * 512 (256; 4 waves, one a SIMD), unpadded; the 16-byte unit u of row r is
- * kept in slot u ^ swz(r), swz(r) = rotl4(r mod 16), which changes the
- * unit's low 4 bits only. A load instruction fills 1 KB (4 or 2 rows)
- * contiguously, so lane i fetches the unit that belongs in its slot. A row
- * is a whole number of 256-byte bank rounds, so a slot's banks depend on
- * slot mod 16 alone, and the swizzle keeps both operand reads free of bank
- * conflicts: a score operand reads one unit of 16 consecutive rows (swz is
- * a bijection on them), a transposed value read two neighbouring units of 4
- * consecutive rows (swz(r) >> 1 differs across the 4, so the 8 slots
- * differ).
+ * kept in slot u ^ swz(r), which changes the unit's low 4 bits only. A load
+ * instruction fills 1 KB (4 or 2 rows) contiguously, so lane i fetches the
+ * unit that belongs in its slot. A row is a whole number of 256-byte bank
+ * rounds, so a slot's banks depend on slot mod 16 alone, and the swizzle
+ * keeps both operand reads free of bank conflicts:
+ *   - a score operand read takes one unit of 16 consecutive rows a
+ *     16-lane pass: swz is a bijection on r mod 16;
+ *   - a transposed value read takes units 4 c .. 4 c + 3 of 4 consecutive
+ *     rows 4 k .. 4 k + 3 a 32-lane pass (256 bytes): swz(r) = the two
+ *     2-bit halves of r mod 16 swapped, so those 4 rows differ in the
+ *     slot's bits 2-3 and the 16 units fill 16 slots. (rotl4(r mod 16)
+ *     left rows r and r + 1 on the same 8 slots: SQ_LDS_BANK_CONFLICT
+ *     counted 2 cycles a value read, a third of the LDS-active cycles;
+ *     with this swizzle it counts none, at the same kernel time.)
  *
- * Two buffer pairs, as distinct arrays, and the tile loop unrolled by two:
- * the compiler then sees that reads of one pair never touch the loads in
- * flight into the other, and waits for those only at the tile's barrier.
+ * Two buffer pairs, as distinct arrays, and the tile loop unrolled by two.
  */
 /*
  * One 16-byte-a-lane load from global memory straight into LDS
@@ -745,7 +748,7 @@ __device__ __forceinline__ void dma16(const char *gbase, uint32_t voff, char *ld
 __device__ __forceinline__ uint32_t swz(uint32_t r)
 {
     r &= 15;
-    return ((r << 1) | (r >> 3)) & 15;
+    return ((r & 3) << 2) | (r >> 2);
 }
 
 template <int D>
