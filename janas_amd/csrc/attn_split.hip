@@ -747,7 +747,6 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
  */
 constexpr int kMergeGroups = 8;
 constexpr int kMergeLanes = 32;            /* lanes a group */
-constexpr int kMergeBatch = 16;
 
 /* the 4 columns of a float4, one by one */
 __device__ __forceinline__ float &f4e(float4 &v, int e)
@@ -762,8 +761,16 @@ __device__ __forceinline__ float &f4e(float4 &v, int e)
  * pairs enough to fill the GPU with 4 times fewer workgroups (blocks of
  * tokens), 1 when it has few (a decode spreads its loads over more CUs), 8
  * with Q8K.
+ *
+ * NB chunks a group's batch (2, 8 or 16): every load of a batch is issued
+ * at once, and chunks past the row's range load its last chunk again and
+ * enter with weight 0. Those are exact no-ops (the sums start at +0 and
+ * never become -0, so adding 0 x v or 0 x l leaves them as they are), so
+ * a row whose chunks fit one batch gets the same bits from any NB; the
+ * launch takes the smallest NB whose batch holds its longest span, and a
+ * short context does not issue 16 loads a group for a few chunks.
  */
-template <int CPL, bool ONE = false, bool Q8K = false>
+template <int CPL, bool ONE = false, bool Q8K = false, int NB = 16>
 __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 {
     static_assert(CPL == 1 || CPL == 4 || CPL == 8, "1, 4 or 8 columns a lane");
@@ -835,12 +842,12 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 #pragma unroll
     for (int u = 0; u < NV; u++)
         ag[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t i0 = g; i0 < nc; i0 += kMergeGroups * kMergeBatch) {
-        float2 ml[kMergeBatch];
-        float4 v[kMergeBatch][NV];
+    for (uint32_t i0 = g; i0 < nc; i0 += kMergeGroups * NB) {
+        float2 ml[NB];
+        float4 v[NB][NV];
         /* branch-free: chunks past the range read the last one, weight 0 */
 #pragma unroll
-        for (int b = 0; b < kMergeBatch; b++) {
+        for (int b = 0; b < NB; b++) {
             const uint32_t i = i0 + kMergeGroups * b < nc ? i0 + kMergeGroups * b : nc - 1;
             const uint64_t pr = base + (uint64_t)i * R;
             ml[b] = *(const float2 *)(A.part_ml + pr * 2);
@@ -855,7 +862,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
         }
         float mb = mg;
 #pragma unroll
-        for (int b = 0; b < kMergeBatch; b++)
+        for (int b = 0; b < NB; b++)
             if (i0 + kMergeGroups * b < nc)
                 mb = fmaxf(mb, ml[b].x);
         /* the batch's sums, against the group's new largest score (scores
@@ -866,7 +873,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
         for (int e = 0; e < CPL; e++)
             f4e(ag[e / 4], e % 4) *= f;
 #pragma unroll
-        for (int b = 0; b < kMergeBatch; b++) {
+        for (int b = 0; b < NB; b++) {
             const float wgt = i0 + kMergeGroups * b < nc ? __builtin_amdgcn_exp2f(ml[b].x - mb) : 0.0f;
             lg += wgt * ml[b].y;
 #pragma unroll
@@ -1052,24 +1059,39 @@ uint32_t merge_cols(uint64_t pairs, uint32_t hd)
     return pairs * ((hd + 127) / 128) >= kMergeFill ? 128 : 32;
 }
 
-hipError_t launch_merge(const SplitArgs &a, uint32_t n_wg, hipStream_t s)
+template <int NB>
+hipError_t launch_merge_nb(const SplitArgs &a, uint32_t n_wg, hipStream_t s)
 {
     const bool one = a.n_seqs == 1;
     if (a.merge_cols == kMergeQ8k && one)
-        hipLaunchKernelGGL((merge_kernel<8, true, true>), dim3(n_wg), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((merge_kernel<8, true, true, NB>), dim3(n_wg), dim3(256), 0, s, a);
     else if (a.merge_cols == kMergeQ8k)
-        hipLaunchKernelGGL((merge_kernel<8, false, true>), dim3(n_wg), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((merge_kernel<8, false, true, NB>), dim3(n_wg), dim3(256), 0, s, a);
     else if (a.merge_cols == 128 && one)
-        hipLaunchKernelGGL((merge_kernel<4, true>), dim3(n_wg), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((merge_kernel<4, true, false, NB>), dim3(n_wg), dim3(256), 0, s, a);
     else if (a.merge_cols == 128)
-        hipLaunchKernelGGL(merge_kernel<4>, dim3(n_wg), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((merge_kernel<4, false, false, NB>), dim3(n_wg), dim3(256), 0, s, a);
     else if (a.merge_cols == 32 && one)
-        hipLaunchKernelGGL((merge_kernel<1, true>), dim3(n_wg), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((merge_kernel<1, true, false, NB>), dim3(n_wg), dim3(256), 0, s, a);
     else if (a.merge_cols == 32)
-        hipLaunchKernelGGL(merge_kernel<1>, dim3(n_wg), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((merge_kernel<1, false, false, NB>), dim3(n_wg), dim3(256), 0, s, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
+}
+
+hipError_t launch_merge(const SplitArgs &a, uint32_t n_wg, hipStream_t s)
+{
+    /* a row reads at most its sequence's span of chunks: the batch that
+       holds the launch's longest span in one round */
+    uint32_t span = 0;
+    for (uint32_t i = 0; i < a.n_seqs && i < kMaxSeqs; i++)
+        span = a.seq[i].span > span ? a.seq[i].span : span;
+    if (span <= kMergeGroups * 2)
+        return launch_merge_nb<2>(a, n_wg, s);
+    if (span <= kMergeGroups * 8)
+        return launch_merge_nb<8>(a, n_wg, s);
+    return launch_merge_nb<16>(a, n_wg, s);
 }
 
 }  // namespace janas
