@@ -26,7 +26,8 @@
  *                  share an L2).
  *   merge kernel   one workgroup per (token, query head, 32 or 128 columns): the
  *                  ordered merge of the chunk partials (8 groups of chunks in
- *                  parallel, each in batches of 16, combined in a fixed
+ *                  parallel, each in batches of 2, 8 or 16 by the
+ *                  launch's longest span, combined in a fixed
  *                  tree), the output gate sigmoid(g) * o (model_attn.c:
  *                  159-170) fused in.
  *
