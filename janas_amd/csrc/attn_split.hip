@@ -1029,8 +1029,11 @@ uint32_t split_mt(int kv, uint32_t hd, uint32_t tiles)
        32 rows) measured slower than two: each wave's chain of products and
        softmax grows with its tiles, and this kernel is bound by that chain,
        not by the matrix cores' rate (8 drafts over 8k positions, 32 / 8 /
-       128: one tile 15.1 us, two 14.1, four 16.2). Above 128 the sums of
-       two tiles would not fit beside the staged rows. */
+       128: one tile 15.1 us, two 14.1, four 16.2). Four for blocks of 16
+       tokens or more only was no better: at one wave a SIMD (215 + 192
+       registers) 64 tokens at 4096 positions took 67.7 us against 47.5,
+       the same bits. Above 128 the sums of two tiles would not fit beside
+       the staged rows. */
     if (kv == kF32 || hd > 128)
         return 1;
     uint32_t mt = 1;
