@@ -305,6 +305,25 @@ def test_large_block_equals_tokens(kv, gpu):
     assert within(err, bar, "vs oracle")
 
 
+@pytest.mark.parametrize("L,pos0", [(4160, 4088), (16448, 16376)])
+def test_block_across_merge_batch_sizes_equals_tokens(L, pos0, gpu):
+    """The merge loads a group's chunks in batches of 2, 8 or 16 by the
+    launch's longest span (up to 16, 64 chunks). A block at positions
+    4088..4103 spans 17 chunks (batches of 8) while its first tokens alone
+    span 16 (batches of 2); one at 16376..16391 spans 65 (16) against 64
+    (8). Chunks past a row's range enter with weight 0, so the block
+    equals its tokens bit for bit all the same."""
+    c = block_case(KV_F16, L=L, n=16, seed=8700 + L)
+    blk = run_block(c, KV_F16, gpu, pos0)
+    one = run_block(c, KV_F16, gpu, pos0, per_token=True)
+    assert np.array_equal(blk.view(np.int32), one.view(np.int32))
+    ref = orc.run(c["q"], c["k"], c["v"], None, None, n_head=c["h"],
+                  n_kv=c["n_kv"], hd=c["hd"], pos0=pos0, kv=KV_F16, threads=16)
+    err = abs_err(blk, ref)
+    print(f"block at {pos0}: max abs err {err:.2e}")
+    assert within(err, TOL_F16_ABS, "block vs oracle")
+
+
 # (cache, heads, KV heads, head size, tokens, scores): a KV head's rows fill
 # two 8-row tiles only in part (15, 12, 9 and 16 rows), so one workgroup
 # takes both, while a token alone (at most 8 rows) takes one tile a
