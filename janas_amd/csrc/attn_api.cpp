@@ -725,7 +725,7 @@ int run_prefill_launch(janas_attn *a, int kv, int gate_mode,
     return JANAS_ATTN_OK;
 }
 
-/* int8 / int16 prompts of at least kDqTokens tokens at head sizes 72..256
+/* int8 / int16 prompts of at least kDqTokens tokens at head sizes up to 256
    run over an f16 copy of the rows they see: one pass writes f16(x *
    scale) - the numbers the register-staged kernel would stage - and the
    f16 kernels (loads straight into LDS, two halves for short calls) take
@@ -806,7 +806,7 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
     if (!prefill_supported(kv, a->hd))
         return JANAS_ATTN_ENOTSUP;
     const bool dq = (kv == kI8 || kv == kI16) && !fixed &&
-                    prefill_supported(kF16, a->hd) && a->hd > 64 && a->hd <= 256;
+                    prefill_supported(kF16, a->hd) && a->hd <= 256;
     if (!dq)
         return run_prefill_launch(a, kv, gate_mode, seqs, n_seqs, stream, fixed);
     /* the long ones one by one over the f16 copy, the others as they are */

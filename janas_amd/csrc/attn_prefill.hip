@@ -27,7 +27,7 @@
  *               64 positions: the tile's fixed costs (barriers, the row
  *               maximum's exchange) spread over twice the products (+3 %).
  *               Two kernels differ only in how a tile reaches LDS:
- *               prefill_dma_kernel (f16, head sizes 72..256) loads it
+ *               prefill_dma_kernel (f16, head sizes up to 256) loads it
  *               straight from memory into XOR-swizzled LDS rows
  *               (global_load_lds_dwordx4; one barrier a tile) and keeps its
  *               operand reads a k-step ahead of the products;
@@ -700,17 +700,18 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_kernel(const PrefillA
 }
 
 /*
- * The f16 kernel for head sizes 72..256: the next tile goes straight from
- * HBM (or L2) into LDS with global_load_lds_dwordx4 while this tile is
+ * The f16 kernel for head sizes up to 256: the next tile goes straight
+ * from HBM (or L2) into LDS with global_load_lds_dwordx4 while this tile is
  * computed - no staging registers, no LDS stores, one barrier a tile.
  *
- * A tile is 128 rows of 256 bytes (head size 128; 8 waves) or 64 rows of
- * 512 (256; 4 waves, one a SIMD), unpadded; the 16-byte unit u of row r is
- * kept in slot u ^ swz(r), which changes the unit's low 4 bits only. A load
- * instruction fills 1 KB (4 or 2 rows) contiguously, so lane i fetches the
- * unit that belongs in its slot. A row is a whole number of 256-byte bank
- * rounds, so a slot's banks depend on slot mod 16 alone, and the swizzle
- * keeps both operand reads free of bank conflicts:
+ * A tile is 128 rows of 128 or 256 bytes (head size 64 or 128; 8 waves) or
+ * 64 rows of 512 (256; 4 waves, one a SIMD), unpadded; the 16-byte unit u
+ * of row r is kept in slot u ^ swz(r), which changes the unit's low 4 (3)
+ * bits only. A load instruction fills 1 KB (8, 4 or 2 rows) contiguously,
+ * so lane i fetches the unit that belongs in its slot. At head sizes 128
+ * and 256 a row is a whole number of 256-byte bank rounds, so a slot's
+ * banks depend on slot mod 16 alone, and the swizzle keeps both operand
+ * reads free of bank conflicts (at 64 two rows share a round: swz<64>):
  *   - a score operand read takes one unit of 16 consecutive rows a
  *     16-lane pass: swz is a bijection on r mod 16;
  *   - a transposed value read takes units 4 c .. 4 c + 3 of 4 consecutive
@@ -745,16 +746,23 @@ __device__ __forceinline__ void dma16(const char *gbase, uint32_t voff, char *ld
                  :: "s"(__builtin_amdgcn_readfirstlane(m0)), "v"(voff), "s"(gbase));
 }
 
-__device__ __forceinline__ uint32_t swz(uint32_t r)
+template <int D> __device__ __forceinline__ uint32_t swz(uint32_t r)
 {
     r &= 15;
-    return ((r & 3) << 2) | (r >> 2);
+    if constexpr (D == 64) {
+        /* rows of 128 bytes: rows r and r + 1 share a bank round, so each
+           parity of r must fill the 8 slots (score reads), and rows 4 k
+           and 4 k + 2 must differ in the slot's bit 2 (value reads) */
+        return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    } else {
+        return ((r & 3) << 2) | (r >> 2);
+    }
 }
 
 template <int D>
 __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const PrefillArgs A)
 {
-    static_assert(D == 128 || D == 256, "rows of 16 or 32 units");
+    static_assert(D == 64 || D == 128 || D == 256, "rows of 8, 16 or 32 units");
     constexpr uint32_t kW = PCfg<D>::W, kTile = PCfg<D>::TILE;
     constexpr uint32_t RB = D * 2;              /* bytes a row */
     constexpr uint32_t UPR = RB / 16;           /* 16-byte units a row */
@@ -779,13 +787,13 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
 
     /* loads: instruction j of wave w fills the RPI rows from
        RPI (w + W j) (1 KB), lane i row RPI (w + W j) + i / UPR, slot
-       i % UPR (the unit slot ^ swz(row)); columns past hd read column 0
+       i % UPR (the unit slot ^ swz<D>(row)); columns past hd read column 0
        (their products meet zero query columns, or are not stored) */
     const uint32_t drow = RPI * w + lane / UPR;
     uint32_t dcol[NJ];
 #pragma unroll
     for (int j = 0; j < (int)NJ; j++) {
-        const uint32_t unit = (lane % UPR) ^ swz(drow + RPI * kW * j);
+        const uint32_t unit = (lane % UPR) ^ swz<D>(drow + RPI * kW * j);
         dcol[j] = unit * 8 < hd ? unit * 8 : 0;
     }
     /* held in registers: read through P.sq inside the loop they would be
@@ -837,14 +845,14 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
     uint32_t koff[D / 16];
 #pragma unroll
     for (int s = 0; s < D / 16; s++)
-        koff[s] = l32 * RB + (((2 * s + g) ^ swz(l16)) * 16);
+        koff[s] = l32 * RB + (((2 * s + g) ^ swz<D>(l16)) * 16);
     const uint32_t vrow = 4 * g + (l16 >> 2);
     const uint32_t u0 = 2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1);
     uint32_t vxo[CT], vyo[CT];
 #pragma unroll
     for (int c = 0; c < CT; c++) {
-        vxo[c] = vrow * RB + (((4 * c + u0) ^ swz(vrow)) * 16) + (l16 & 1) * 8;
-        vyo[c] = (vrow + 8) * RB + (((4 * c + u0) ^ swz(vrow + 8)) * 16) + (l16 & 1) * 8;
+        vxo[c] = vrow * RB + (((4 * c + u0) ^ swz<D>(vrow)) * 16) + (l16 & 1) * 8;
+        vyo[c] = (vrow + 8) * RB + (((4 * c + u0) ^ swz<D>(vrow + 8)) * 16) + (l16 & 1) * 8;
     }
 
     float m = -INFINITY, lsum = 0.0f;
@@ -997,7 +1005,7 @@ __global__ __launch_bounds__((PCfg<D, true>::W) * 64) void prefill_half_kernel(c
     uint32_t dcol[NJ];
 #pragma unroll
     for (int j = 0; j < (int)NJ; j++) {
-        const uint32_t unit = (lane % UPR) ^ swz(drow + RPI * kGW * j);
+        const uint32_t unit = (lane % UPR) ^ swz<D>(drow + RPI * kGW * j);
         dcol[j] = unit * 8 < hd ? unit * 8 : 0;
     }
     const char *const kg = (const char *)sq.k, *const vg = (const char *)sq.v;
@@ -1018,14 +1026,14 @@ __global__ __launch_bounds__((PCfg<D, true>::W) * 64) void prefill_half_kernel(c
     uint32_t koff[D / 16];
 #pragma unroll
     for (int s = 0; s < D / 16; s++)
-        koff[s] = l32 * RB + (((2 * s + g) ^ swz(l16)) * 16);
+        koff[s] = l32 * RB + (((2 * s + g) ^ swz<D>(l16)) * 16);
     const uint32_t vrow = 4 * g + (l16 >> 2);
     const uint32_t u0 = 2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1);
     uint32_t vxo[CT], vyo[CT];
 #pragma unroll
     for (int c = 0; c < CT; c++) {
-        vxo[c] = vrow * RB + (((4 * c + u0) ^ swz(vrow)) * 16) + (l16 & 1) * 8;
-        vyo[c] = (vrow + 8) * RB + (((4 * c + u0) ^ swz(vrow + 8)) * 16) + (l16 & 1) * 8;
+        vxo[c] = vrow * RB + (((4 * c + u0) ^ swz<D>(vrow)) * 16) + (l16 & 1) * 8;
+        vyo[c] = (vrow + 8) * RB + (((4 * c + u0) ^ swz<D>(vrow + 8)) * 16) + (l16 & 1) * 8;
     }
 
     float m = -INFINITY, lsum = 0.0f;
@@ -1192,7 +1200,7 @@ hipError_t launch_d(const PrefillArgs &a, hipStream_t s)
     }
     if (a.halves)
         return hipErrorInvalidValue;
-    if constexpr (T == kF16 && (D == 128 || D == 256))
+    if constexpr (T == kF16 && (D == 64 || D == 128 || D == 256))
         hipLaunchKernelGGL((prefill_dma_kernel<D>), dim3(a.n_wg), dim3(PCfg<D>::W * 64), 0, s, a);
     else
         hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(a.n_wg), dim3(PCfg<D>::W * 64), 0, s, a);

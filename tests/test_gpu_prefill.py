@@ -388,7 +388,7 @@ def quantized(seed, n_kv, cap, hd, wide):
 def test_prefill_quantized_cache(gpu, wide, geom):
     """int8 / int16 caches with their scales (the engine's own format) on
     the MFMA path: rows dequantized into f16 as tiles are staged, or, for
-    prompts of 256 tokens or more at head sizes 72..256, into an f16 copy
+    prompts of 256 tokens or more at head sizes up to 256, into an f16 copy
     first; the bar is the f16 one."""
     h, kvh, hd, cap = geom["n_head"], geom["n_kv"], geom["hd"], geom["cap"]
     n, pos0 = geom["n"], geom["pos0"]
@@ -420,13 +420,15 @@ def test_prefill_quantized_cache(gpu, wide, geom):
     assert within(err, TOL_F16_ABS, "vs oracle")
 
 
+@pytest.mark.parametrize("hd", [128, 64])
 @pytest.mark.parametrize("wide", [False, True])
-def test_prefill_quantized_long_prompt_f16_copy(gpu, wide):
+def test_prefill_quantized_long_prompt_f16_copy(gpu, wide, hd):
     """A long int8 / int16 prompt runs the f16 kernels over an f16 copy of
     its rows (f16(x * scale), the numbers the register-staged kernel
     stages): bitwise equal to the allocation-free entry point, which keeps
-    the register-staged kernel, and within the bar of the restatement."""
-    h, kvh, hd, n, pos0 = 32, 8, 128, 2048, 0
+    the register-staged kernel, and within the bar of the restatement.
+    Head size 64 takes the DMA kernel's 128-byte rows."""
+    h, kvh, n, pos0 = 32, 8, 2048, 0
     k, ks = quantized(9100 + wide, kvh, n, hd, wide)
     v, vs = quantized(9102 + wide, kvh, n, hd, wide)
     q = normal(9104, n * h * hd).reshape(n, h, hd)
@@ -444,7 +446,7 @@ def test_prefill_quantized_long_prompt_f16_copy(gpu, wide):
     ref = orc.run(q.astype(np.float32), k, v, ks, vs, n_head=h, n_kv=kvh,
                   hd=hd, pos0=pos0, kv=kv, threads=threads(), block=64)
     err = abs_err(outs[0], ref)
-    print(f"f16 copy {'int16' if wide else 'int8'}: max abs err {err:.2e}")
+    print(f"f16 copy {'int16' if wide else 'int8'} hd {hd}: max abs err {err:.2e}")
     assert within(err, TOL_F16_ABS, "vs oracle")
 
 
