@@ -725,13 +725,17 @@ int run_prefill_launch(janas_attn *a, int kv, int gate_mode,
     return JANAS_ATTN_OK;
 }
 
-/* int8 / int16 prompts of at least kDqTokens tokens at head sizes up to 256
+/* int8 / int16 prompts of at least dq_tokens(hd) tokens (256, or 512 at
+   head sizes up to 64) at head sizes up to 256
    run over an f16 copy of the rows they see: one pass writes f16(x *
    scale) - the numbers the register-staged kernel would stage - and the
    f16 kernels (loads straight into LDS, two halves for short calls) take
    it from there. The pass is linear in the positions, the prompt's work
-   quadratic. */
+   quadratic. At head size 64 the copy's extra launch outweighs the
+   faster kernel below 512 tokens (256 tokens: 13.5 against 12.5 us; 512:
+   17.3 against 17.5; 1024: 25.4 against 27.7, 32 / 8 / 64). */
 constexpr uint32_t kDqTokens = 256;
+inline uint32_t dq_tokens(uint32_t hd) { return hd <= 64 ? 2 * kDqTokens : kDqTokens; }
 
 int ensure_dq(janas_attn *a, size_t bytes, hipStream_t stream)
 {
@@ -816,7 +820,7 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
         uint32_t nr = 0;
         for (uint32_t i = 0; i < m; i++) {
             const janas_attn_seq &q = seqs[s0 + i];
-            if (q.n >= kDqTokens && q.k && q.v && q.ks && q.vs) {
+            if (q.n >= dq_tokens(a->hd) && q.k && q.v && q.ks && q.vs) {
                 /* no memory for the copy: the register-staged kernel,
                    which needs none */
                 int rc = run_prefill_dq(a, kv, gate_mode, q, stream);
