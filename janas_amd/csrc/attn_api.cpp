@@ -241,18 +241,21 @@ struct Parts {
     bool fixed;
 };
 
-int get_parts(janas_attn *a, uint64_t rows, hipStream_t stream, bool fixed, Parts &p)
+int get_parts(janas_attn *a, uint64_t rows, hipStream_t stream, bool fixed, Parts &p,
+              uint64_t reserve = 0)
 {
     if (fixed) {
+        /* past the first `reserve` bytes of the array (a prompt's exact
+           copy, 256-byte aligned) */
         char *base = (char *)scratch_ptr(a->dev);
         if (!base)
             return JANAS_ATTN_EDEVICE;
         /* ml: rows x 2 floats, then acc (256-byte aligned): rows x hd */
         const uint64_t ml_bytes = (rows * 2 * sizeof(float) + 255) / 256 * 256;
-        if (ml_bytes + rows * a->hd * sizeof(float) > JANAS_ATTN_NOALLOC_BYTES)
+        if (reserve + ml_bytes + rows * a->hd * sizeof(float) > JANAS_ATTN_NOALLOC_BYTES)
             return JANAS_ATTN_ERANGE;
-        p.ml = (float *)base;
-        p.acc = (float *)(base + ml_bytes);
+        p.ml = (float *)(base + reserve);
+        p.acc = (float *)(base + reserve + ml_bytes);
         p.fixed = true;
         return JANAS_ATTN_OK;
     }
@@ -613,14 +616,14 @@ void choose_way_dev(janas_attn *a, int kv, const janas_attn_seq *seqs, uint32_t 
    sequence alone, so a sequence's result is the same in any launch. */
 constexpr uint32_t kSegTiles = 6;
 
-uint32_t prefill_segments(const janas_attn *a, const SeqDesc &d, bool halves)
+uint32_t prefill_segments(const janas_attn *a, const SeqDesc &d, bool halves, int exact)
 {
     const uint64_t blocks =
-        (uint64_t)a->n_kv * prefill_row_blocks(d.n, a->group, a->hd, halves);
+        (uint64_t)a->n_kv * prefill_row_blocks(d.n, a->group, a->hd, halves, exact);
     if (blocks >= a->cus)
         return 1;
     /* the key tiles of the latest row block, which sees the most */
-    const uint32_t tile = prefill_tile(a->hd, halves);
+    const uint32_t tile = prefill_tile(a->hd, halves, exact);
     const uint32_t last = d.pos0 + d.n - 1;
     const uint32_t lo = a->window && last + 1 > a->window ? last + 1 - a->window : 0;
     const uint32_t nt = (d.end - 1) / tile - lo / tile + 1;
@@ -643,16 +646,18 @@ bool prefill_halves(const janas_attn *a, int kv, const SeqDesc &d)
 {
     if (!prefill_halves_supported(kv, a->hd))
         return false;
-    const uint64_t wg = (uint64_t)a->n_kv * prefill_segments(a, d, false) *
+    const uint64_t wg = (uint64_t)a->n_kv * prefill_segments(a, d, false, 0) *
                         prefill_row_blocks(d.n, a->group, a->hd, false);
     return wg < a->cus;
 }
 
 /* The sequences in launches of up to kMaxSeqs, those that take the
-   two-halves kernel first, then the others. */
+   two-halves kernel first, then the others. exact: the sequences' k and v
+   are the exact copies (run_prefill_x) of int8 (1) or int16 (2) caches;
+   reserve: bytes of the fixed array they take (fixed only). */
 int run_prefill_launch(janas_attn *a, int kv, int gate_mode,
                        const janas_attn_seq *seqs, uint32_t n_seqs, hipStream_t stream,
-                       bool fixed)
+                       bool fixed, int exact = 0, uint64_t reserve = 0)
 {
     for (int hv = 1; hv >= 0; hv--) {
         for (uint32_t i = 0; i < n_seqs;) {
@@ -666,14 +671,14 @@ int run_prefill_launch(janas_attn *a, int kv, int gate_mode,
                 int rc = describe(a, kv, seqs[i], d);
                 if (rc)
                     return rc;
-                if (prefill_halves(a, kv, d) != (hv == 1))
+                if ((!exact && prefill_halves(a, kv, d)) != (hv == 1))
                     continue;
                 d.wg0 = wg;
                 d.mg0 = mg;
-                d.nseg = prefill_segments(a, d, hv == 1);
+                d.nseg = prefill_segments(a, d, hv == 1, exact);
                 d.part0 = 0;
                 uint64_t nwg = (uint64_t)a->n_kv * d.nseg *
-                               prefill_row_blocks(d.n, a->group, a->hd, hv == 1);
+                               prefill_row_blocks(d.n, a->group, a->hd, hv == 1, exact);
                 uint64_t nmg = 0;
                 if (d.nseg > 1) {
                     /* partial rows from part0: (token, head) major, segment minor */
@@ -691,7 +696,7 @@ int run_prefill_launch(janas_attn *a, int kv, int gate_mode,
                 break;
             Parts pt{nullptr, nullptr, fixed};
             if (rows) {
-                int rc = get_parts(a, rows, stream, fixed, pt);
+                int rc = get_parts(a, rows, stream, fixed, pt, reserve);
                 if (rc)
                     return rc;
             }
@@ -708,6 +713,7 @@ int run_prefill_launch(janas_attn *a, int kv, int gate_mode,
             args.ring = a->ring;
             args.gate_mode = gate_mode;
             args.halves = hv;
+            args.exact = exact;
             ProfEv *ev = fixed ? nullptr : prof_begin(a, 2, stream);
             hipError_t e = launch_prefill(kv, args, stream);
             if (e == hipSuccess && mg)
@@ -725,18 +731,8 @@ int run_prefill_launch(janas_attn *a, int kv, int gate_mode,
     return JANAS_ATTN_OK;
 }
 
-/* int8 / int16 prompts of at least dq_tokens(hd) tokens (256, or 512 at
-   head sizes up to 64) at head sizes up to 256
-   run over an f16 copy of the rows they see: one pass writes f16(x *
-   scale) - the numbers the register-staged kernel would stage - and the
-   f16 kernels (loads straight into LDS, two halves for short calls) take
-   it from there. The pass is linear in the positions, the prompt's work
-   quadratic. At head size 64 the copy's extra launch outweighs the
-   faster kernel below 512 tokens (256 tokens: 13.5 against 12.5 us; 512:
-   17.3 against 17.5; 1024: 25.4 against 27.7, 32 / 8 / 64). */
-constexpr uint32_t kDqTokens = 256;
-inline uint32_t dq_tokens(uint32_t hd) { return hd <= 64 ? 2 * kDqTokens : kDqTokens; }
-
+/* The exact kernel's copies (K planes, then V planes) in instance memory,
+   grown on demand and ordered across streams as the partials. */
 int ensure_dq(janas_attn *a, size_t bytes, hipStream_t stream)
 {
     if (bytes <= a->dq_bytes)
@@ -763,44 +759,79 @@ int ensure_dq(janas_attn *a, size_t bytes, hipStream_t stream)
     return JANAS_ATTN_OK;
 }
 
-/* One int8 / int16 sequence over the f16 copy of its visible rows. */
-int run_prefill_dq(janas_attn *a, int kv, int gate_mode, const janas_attn_seq &s,
-                   hipStream_t stream)
+/* int8 / int16 caches at head sizes up to 256 (the reference's FLOAT way,
+   attention.c:107-145: the cached integers exact, f32 arithmetic): each
+   sequence's visible rows - chunks c0 .. of every KV head, as the split path
+   counts them - are copied as f16 planes whose sum is the integer exactly
+   (launch_xcopy: linear in the positions), and prefill_exact_kernel takes
+   them with the query and the weights as two f16 planes each. The copies
+   live in instance memory, or, for the allocation-free entry point (fixed),
+   at the start of the device's fixed array, the partials after them. */
+int run_prefill_x(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
+                  uint32_t n_seqs, hipStream_t stream, bool fixed)
 {
-    SeqDesc d;
-    int rc = describe(a, kv, s, d);
-    if (rc)
-        return rc;
-    const size_t bytes = (size_t)a->n_kv * s.cap * a->hd * sizeof(_Float16);
-    rc = ensure_dq(a, bytes, stream);
-    if (!rc)
-        rc = part_sync(a, stream);
-    if (rc)
-        return rc;
-    DqArgs q;
-    q.k = s.k;
-    q.v = s.v;
-    q.ks = s.ks;
-    q.vs = s.vs;
-    q.k16 = (_Float16 *)a->dq_k;
-    q.v16 = (_Float16 *)a->dq_v;
-    q.n_kv = a->n_kv;
-    q.cap = s.cap;
-    q.hd = a->hd;
-    q.ring = a->ring;
-    /* the chunks the call sees, as the split path counts them */
-    q.p0 = d.c0 * kChunk;
-    q.np = d.end - q.p0;
-    ProfEv *ev = prof_begin(a, 2, stream);
-    hipError_t e = launch_dequant(kv, q, stream);
-    prof_end(ev, stream);
-    if (e != hipSuccess)
-        return hip_err(e, "dequant launch");
-    janas_attn_seq s16 = s;
-    s16.k = a->dq_k;
-    s16.v = a->dq_v;
-    s16.ks = s16.vs = nullptr;
-    return run_prefill_launch(a, kF16, gate_mode, &s16, 1, stream, false);
+    const int ex = kv == kI16 ? 2 : 1;
+    for (uint32_t s0 = 0; s0 < n_seqs; s0 += kMaxSeqs) {
+        const uint32_t m = std::min(kMaxSeqs, n_seqs - s0);
+        DqArgs q[kMaxSeqs];
+        size_t off[kMaxSeqs], total = 0;
+        for (uint32_t i = 0; i < m; i++) {
+            const janas_attn_seq &s = seqs[s0 + i];
+            SeqDesc d;
+            int rc = describe(a, kv, s, d);
+            if (rc)
+                return rc;
+            memset(&q[i], 0, sizeof q[i]);
+            q[i].k = s.k;
+            q[i].v = s.v;
+            q[i].n_kv = a->n_kv;
+            q[i].cap = s.cap;
+            q[i].hd = a->hd;
+            q[i].ring = a->ring;
+            q[i].p0 = d.c0 * kChunk;
+            q[i].np = d.end - q[i].p0;
+            off[i] = total;
+            total += ((size_t)ex * a->n_kv * q[i].np * a->hd * sizeof(_Float16) + 255) / 256 * 256;
+        }
+        char *ck, *cv;
+        if (fixed) {
+            char *base = (char *)scratch_ptr(a->dev);
+            if (!base)
+                return JANAS_ATTN_EDEVICE;
+            if (2 * total > JANAS_ATTN_NOALLOC_BYTES)
+                return JANAS_ATTN_ERANGE;
+            ck = base;
+            cv = base + total;
+        } else {
+            int rc = ensure_dq(a, total, stream);
+            if (!rc)
+                rc = part_sync(a, stream);
+            if (rc)
+                return rc;
+            ck = (char *)a->dq_k;
+            cv = (char *)a->dq_v;
+        }
+        janas_attn_seq xs[kMaxSeqs];
+        ProfEv *ev = fixed ? nullptr : prof_begin(a, 2, stream);
+        for (uint32_t i = 0; i < m; i++) {
+            q[i].k16 = (_Float16 *)(ck + off[i]);
+            q[i].v16 = (_Float16 *)(cv + off[i]);
+            hipError_t e = launch_xcopy(kv, q[i], stream);
+            if (e != hipSuccess) {
+                prof_end(ev, stream);
+                return hip_err(e, "copy launch");
+            }
+            xs[i] = seqs[s0 + i];
+            xs[i].k = q[i].k16;
+            xs[i].v = q[i].v16;
+        }
+        prof_end(ev, stream);
+        int rc = run_prefill_launch(a, kv, gate_mode, xs, m, stream, fixed, ex,
+                                    fixed ? 2 * total : 0);
+        if (rc)
+            return rc;
+    }
+    return JANAS_ATTN_OK;
 }
 
 int run_prefill(janas_attn *a, int kv, int gate_mode,
@@ -809,36 +840,9 @@ int run_prefill(janas_attn *a, int kv, int gate_mode,
 {
     if (!prefill_supported(kv, a->hd))
         return JANAS_ATTN_ENOTSUP;
-    const bool dq = (kv == kI8 || kv == kI16) && !fixed &&
-                    prefill_supported(kF16, a->hd) && a->hd <= 256;
-    if (!dq)
-        return run_prefill_launch(a, kv, gate_mode, seqs, n_seqs, stream, fixed);
-    /* the long ones one by one over the f16 copy, the others as they are */
-    janas_attn_seq rest[kMaxSeqs];
-    for (uint32_t s0 = 0; s0 < n_seqs; s0 += kMaxSeqs) {
-        const uint32_t m = std::min(kMaxSeqs, n_seqs - s0);
-        uint32_t nr = 0;
-        for (uint32_t i = 0; i < m; i++) {
-            const janas_attn_seq &q = seqs[s0 + i];
-            if (q.n >= dq_tokens(a->hd) && q.k && q.v && q.ks && q.vs) {
-                /* no memory for the copy: the register-staged kernel,
-                   which needs none */
-                int rc = run_prefill_dq(a, kv, gate_mode, q, stream);
-                if (rc == JANAS_ATTN_ENOMEM)
-                    rc = run_prefill_launch(a, kv, gate_mode, &q, 1, stream, false);
-                if (rc)
-                    return rc;
-            } else {
-                rest[nr++] = q;
-            }
-        }
-        if (nr) {
-            int rc = run_prefill_launch(a, kv, gate_mode, rest, nr, stream, false);
-            if (rc)
-                return rc;
-        }
-    }
-    return JANAS_ATTN_OK;
+    if ((kv == kI8 || kv == kI16) && a->hd <= 256)
+        return run_prefill_x(a, kv, gate_mode, seqs, n_seqs, stream, fixed);
+    return run_prefill_launch(a, kv, gate_mode, seqs, n_seqs, stream, fixed);
 }
 
 int check_call(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,

@@ -92,14 +92,18 @@ struct PrefillArgs {
     int gate_mode;
     int halves;            /* the two-halves kernel (prefill_halves_supported):
                               128 rows a workgroup, two key groups */
+    int exact;             /* int8 / int16 at float accuracy
+                              (prefill_exact_kernel): the planes of the copy
+                              the sequences' k and v point at (1 int8, 2
+                              int16; launch_xcopy), scales from ks / vs */
 };
 
-/* An int8 / int16 cache's rows of positions p0 .. p0 + np - 1 as f16
-   (f16(x * scale)), into a copy laid out as the cache. */
+/* An int8 / int16 cache's rows of positions p0 .. p0 + np - 1 as the
+   exact kernel's f16 planes (xcopy_kernel): plane by plane, row
+   kvh np + (p - p0) of each. */
 struct DqArgs {
-    const void *k, *v;
-    const float *ks, *vs;
-    _Float16 *k16, *v16;   /* [n_kv][cap][hd] */
+    const void *k, *v;     /* the cache, [n_kv][cap][hd] */
+    _Float16 *k16, *v16;   /* the copies, [planes][n_kv][np][hd] */
     uint32_t n_kv, cap, hd, ring;
     uint32_t p0, np;
 };
@@ -189,12 +193,16 @@ int prefill_supported(int kv, uint32_t hd);
 /* row blocks a KV head of an n-token sequence takes (one workgroup each
    per key segment), and the key positions a tile; halves: the two-halves
    kernel's (PrefillArgs::halves) */
-uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd, bool halves);
-uint32_t prefill_tile(uint32_t hd, bool halves);
+uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd, bool halves,
+                            int exact = 0);
+uint32_t prefill_tile(uint32_t hd, bool halves, int exact = 0);
 /* 1 when the two-halves kernel takes this element type and head size */
 int prefill_halves_supported(int kv, uint32_t hd);
-/* dequant_kernel (int8 / int16 rows to f16) */
-hipError_t launch_dequant(int kv, const DqArgs &a, hipStream_t s);
+/* xcopy_kernel: the exact kernel's copy of an int8 / int16 cache's rows
+   p0 .. p0 + np - 1, per KV head from p0, as 1 (int8) or 2 (int16) planes
+   of n_kv x np x hd f16 each; k16 and v16 hold the planes one after the
+   other */
+hipError_t launch_xcopy(int kv, const DqArgs &a, hipStream_t s);
 /* the ordered merge of split sequences' segment partials: a thread takes 4
    columns of one row (a row is one (token, head)), a workgroup
    kPMergeThreads of them; a sequence of n tokens takes pmerge_groups of

@@ -93,11 +93,18 @@ constexpr int kPRows = 32;                 /* query rows a wave */
    compute units idle): the 8 waves are two key groups of 4 over the same
    128 rows, each taking half of the block's key tiles of 64 positions; the
    two halves' states are combined in LDS at the end */
-template <int D, bool HV = false> struct PCfg {
+/* EX (the exact kernel over an int8 / int16 cache, prefill_exact_kernel):
+   the planes each key and value row enters the products as, 1 (int8) or 2
+   (int16); 64-position tiles (32 at head size 256 with two planes, for
+   LDS), and 4 waves, one a SIMD, where two planes' operands would not fit
+   two waves' registers */
+template <int D, bool HV = false, int EX = 0> struct PCfg {
     static_assert(!HV || D == 128, "halves: head sizes 72..128");
-    static constexpr int W = D > 128 ? 4 : 8;
+    static_assert(!HV || !EX, "halves: f16 only");
+    static constexpr int W = D > 128 || (EX == 2 && D > 64) ? 4 : 8;
     static constexpr int GW = HV ? 4 : W;   /* waves a key group */
-    static constexpr int TILE = HV ? 64 : D > 256 ? 32 : D > 128 ? 64 : 128;
+    static constexpr int TILE = EX == 2 && D == 256 ? 32
+                              : HV || EX ? 64 : D > 256 ? 32 : D > 128 ? 64 : 128;
     static constexpr int NPB = TILE / 32;   /* blocks of 32 positions a tile */
     static constexpr int CS = D > 256 ? 2 : 1;  /* column splits of a row */
     static constexpr int OC = D / CS;       /* output columns a wave */
@@ -227,16 +234,17 @@ struct PBlock {
     uint32_t tfirst, tlast;    /* key tiles visited (the segment's) */
     uint32_t seg, nseg;        /* the key segment, of nseg (1: not split) */
     size_t head_row;           /* the KV head's first cache row */
+    uint32_t kvh;              /* the KV head */
     bool rok;                  /* the lane's row exists */
     uint32_t rj, rh;           /* its token and query head */
     uint32_t rlo, rhi;         /* the positions it sees */
     uint32_t col0;             /* the wave's first output column */
 };
 
-template <int D, bool HV = false>
+template <int D, bool HV = false, int EX = 0>
 __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
 {
-    constexpr int kPBlock = PCfg<D, HV>::BLOCK, kTile = PCfg<D, HV>::TILE;
+    constexpr int kPBlock = PCfg<D, HV, EX>::BLOCK, kTile = PCfg<D, HV, EX>::TILE;
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t l32 = lane & 31;
     /* the XCDs in groups of 8 / gcd(n_kv, 8): each group takes whole KV
@@ -287,8 +295,9 @@ __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
         P.tlast = empty ? a : b - 1;
     }
     P.head_row = (size_t)kvh * sq.cap;
+    P.kvh = kvh;
 
-    const uint32_t r = r0 + kPRows * ((w % PCfg<D, HV>::GW) / PCfg<D>::CS) + l32;
+    const uint32_t r = r0 + kPRows * ((w % PCfg<D, HV, EX>::GW) / PCfg<D>::CS) + l32;
     P.col0 = (w % PCfg<D>::CS) * PCfg<D>::OC;
     P.rok = r < R;
     P.rj = (P.rok ? r : r0) / G;
@@ -906,17 +915,458 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
 }
 
 /*
- * The key and value rows of positions p0 .. p0 + np - 1 of every KV head of
- * an int8 / int16 cache as f16, f16(x * scale) - the numbers
- * prefill_kernel stages into LDS (PElem::to_f16) - into a copy laid out as
- * the cache (row kvh cap + p, or p mod cap on a ring), so the f16 kernels
- * can run over a long prompt of the engine's own format. A thread takes 8
- * numbers of one row.
+ * ---- The exact kernel: int8 / int16 caches at float accuracy ----------
+ *
+ * The reference's FLOAT way (attention.c:107-118, :574-627, :761-763,
+ * :135-145) holds int8 keys and values exact and computes in f32, and so
+ * does this pass: the cache's integers enter the products as they are, in
+ * f16 planes whose sum is the cached number exactly (int8: one plane; int16:
+ * x with its low byte cleared, and the low byte), and the query and the
+ * weights as two f16 planes each (x = hi + lo, 22 significant bits), so each
+ * product is exact in the matrix core and summed in f32. The scales stay f32:
+ *   score   s = (sum_i q'_i k_i) * ks[p] * 2^-e,  q' = q * scale * log2(e) * 2^e
+ *           (e puts the row's largest |q'| in [2^13, 2^14): neither plane
+ *           loses bits to f16's range)
+ *   value   o = sum_p (w_p * vs[p]) v_p / sum_p w_p,  the weight and the value
+ *           scale multiplied in f32 before the split into planes
+ * The weights carry a fixed power of two, 2^6 over an int8 cache and 2^14
+ * over int16 (XBias), so that w * vs = w 2^6 max|v| / 127 (or 2^14 max|v| /
+ * 32767) keeps its low plane inside f16's normal range for every weight
+ * that matters (the high plane from 2^-3 up: weights from about 2^-9 of
+ * the row's largest at a value row's largest magnitude of 1); the power
+ * cancels between the sums. A value row's largest magnitude must stay
+ * below 500 (w * vs below f16's 65504 at the lazy maximum's 2^8).
+ *
+ * The keys and values come from a copy of the call's visible rows in those
+ * planes (xcopy_kernel: the integers widened, linear in the positions, laid
+ * out per KV head from the call's first chunk), tiles straight into LDS as in
+ * prefill_dma_kernel, with the same swizzle; the scales of a tile come from
+ * the cache itself (a 4-byte load into LDS a lane, every position clamped to
+ * the rows the block sees, so nothing outside them is read).
+ */
+/* x = hi + lo in f16 (22 significant bits). x is pinned in a register
+   first (an empty asm): left free, the compiler made hi from the f32
+   product x = w * vs for the products, but made it again for lo straight
+   from the exact product (v_fma_mixlo_f16 w, vs, 0: one rounding instead of
+   two) - at a rounding tie the two differ by an f16 unit, and hi + lo
+   missed the weight by twice lo (an error of 2^-10 on one weight in a
+   hundred rows). */
+__device__ __forceinline__ void split_hl(float x, _Float16 &hi, _Float16 &lo)
+{
+    asm volatile("" : "+v"(x));
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+template <int EX> struct XBias {
+    static constexpr float value = EX == 2 ? 14.0f : 6.0f;
+};
+
+/* the loads into LDS of score k-step s when NL are spread over KS steps
+   (load i at step i mod KS), plus the tile's scales at step 0 */
+template <int NL, int KS> constexpr int xloads_at(int s)
+{
+    return (s < NL ? (NL - 1 - s) / KS + 1 : 0) + (s == 0 ? 1 : 0);
+}
+
+/* a scheduling group of n loads (n a constant once the caller's loop is
+   unrolled) */
+__device__ __forceinline__ void sgb_vmem(int n)
+{
+    switch (n) {
+    case 1: __builtin_amdgcn_sched_group_barrier(0x010, 1, 0); break;
+    case 2: __builtin_amdgcn_sched_group_barrier(0x010, 2, 0); break;
+    case 3: __builtin_amdgcn_sched_group_barrier(0x010, 3, 0); break;
+    case 4: __builtin_amdgcn_sched_group_barrier(0x010, 4, 0); break;
+    default: break;
+    }
+}
+
+/* One 4-byte-a-lane load from a 64-bit address straight into LDS
+   (global_load_lds_dword: lane l's 4 bytes land at LDS address m0 + 4 l),
+   written out for the reasons given at dma16. */
+__device__ __forceinline__ void dma4(const void *g, char *lds)
+{
+    const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
+                 :: "s"(__builtin_amdgcn_readfirstlane(m0)), "v"(g));
+}
+
+/* the lane's query row times the score scale, log2(e) and 2^e (its largest
+   magnitude in [2^13, 2^14)) as two f16 planes; returns 2^-e */
+template <int D>
+__device__ __forceinline__ float load_query_x(const PrefillArgs &A, const PBlock &P, h8 *qh,
+                                              h8 *ql)
+{
+#pragma clang fp contract(off)
+    const uint32_t g = (threadIdx.x & 63) >> 5, hd = A.hd;
+    const float *qrow = P.sq->q + ((size_t)P.rj * A.n_head + P.rh) * hd;
+    const float f = A.scale * kLog2e;
+    float mx = 0.0f;
+#pragma unroll
+    for (int s = 0; s < D / 16; s++) {
+        const uint32_t c = 16 * s + 8 * g;
+        if (P.rok && c < hd) {
+            const float4 x0 = *(const float4 *)(qrow + c);
+            const float4 x1 = *(const float4 *)(qrow + c + 4);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x0.x * f), fabsf(x0.y * f)),
+                                 fmaxf(fabsf(x0.z * f), fabsf(x0.w * f))));
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x1.x * f), fabsf(x1.y * f)),
+                                 fmaxf(fabsf(x1.z * f), fabsf(x1.w * f))));
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    int ex = 0;
+    if (mx > 0.0f && mx < INFINITY) {
+        frexpf(mx, &ex);
+        ex = 14 - ex;
+        ex = ex > 100 ? 100 : ex < -100 ? -100 : ex;
+    }
+    const float up = ldexpf(1.0f, ex);
+#pragma unroll
+    for (int s = 0; s < D / 16; s++) {
+        const uint32_t c = 16 * s + 8 * g;
+        const bool cok = P.rok && c < hd;
+        const float4 x0 = *(const float4 *)(qrow + (cok ? c : 0));
+        const float4 x1 = *(const float4 *)(qrow + (cok ? c + 4 : 0));
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            _Float16 hi, lo;
+            split_hl(cok ? (xs[e] * f) * up : 0.0f, hi, lo);
+            qh[s][e] = hi;
+            ql[s][e] = lo;
+        }
+    }
+    return ldexpf(1.0f, -ex);
+}
+
+/*
+ * One key tile of the exact kernel for the lane's row: the tile pass of
+ * tile_pass with planes. kop(s, b, p): plane p of the score operand (K rows
+ * 32 b + l % 32, columns 16 s + 8 (l / 32) ..); vop(ks, c, p): plane p of the
+ * value operand; sop(which, b, j): the key (which 0) or value (1) scales of
+ * positions 32 b + 8 j + 4 (l / 32) + 0..3 of the tile; lop(s): the loads
+ * of score k-step s. Operands are read one k-step ahead of the products.
+ */
+template <int D, int EX, int NL, class KOp, class VOp, class SOp, class LOp>
+__device__ __forceinline__ void tile_pass_x(uint32_t p0, const PBlock &P, const h8 *qh,
+                                            const h8 *ql, float qsc, float &m, float &lsum,
+                                            f16x *o, KOp kop, VOp vop, SOp sop, LOp lop)
+{
+#pragma clang fp contract(off)
+    using C = PCfg<D, false, EX>;
+    constexpr int kNPB = C::NPB, kTile = C::TILE, NP = EX;
+    constexpr int KS = D / 16, CT = D / 32;
+    constexpr float kB = XBias<EX>::value;
+    const uint32_t g = (threadIdx.x & 63) >> 5;
+    const float mref = m == -INFINITY ? 0.0f : m;
+
+    f16x sacc[kNPB];
+#pragma unroll
+    for (int b = 0; b < kNPB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            sacc[b][i] = 0.0f;
+    h8 ka[2][kNPB][NP];
+#pragma unroll
+    for (int b = 0; b < kNPB; b++)
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+            ka[0][b][p] = kop(0, b, p);
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+        lop(s);
+        if (s + 1 < KS)
+#pragma unroll
+            for (int b = 0; b < kNPB; b++)
+#pragma unroll
+                for (int p = 0; p < NP; p++)
+                    ka[(s + 1) & 1][b][p] = kop(s + 1, b, p);
+#pragma unroll
+        for (int b = 0; b < kNPB; b++)
+#pragma unroll
+            for (int p = 0; p < NP; p++) {
+                sacc[b] = mfma(ka[s & 1][b][p], qh[s], sacc[b]);
+                sacc[b] = mfma(ka[s & 1][b][p], ql[s], sacc[b]);
+            }
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, kNPB * NP, 0);
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+        sgb_vmem(xloads_at<NL, KS>(s));
+        if (s + 1 < KS)
+            __builtin_amdgcn_sched_group_barrier(0x100, kNPB * NP, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * kNPB * NP, 0);
+    }
+
+    /* the key scales, the query's 2^-e, and the weights' 2^kB less the
+       row's maximum so far */
+    const float bm = kB - mref;
+#pragma unroll
+    for (int b = 0; b < kNPB; b++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 z = sop(0, b, j);
+            const float zs[4] = {z.x, z.y, z.z, z.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                sacc[b][4 * j + e] = fmaf(sacc[b][4 * j + e], zs[e] * qsc, bm);
+        }
+
+    const bool partial = !(P.rlo <= p0 && P.rhi >= p0 + kTile - 1);
+    if (__any(partial)) {
+#pragma unroll
+        for (int b = 0; b < kNPB; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t p = p0 + 32 * b + 8 * (i / 4) + 4 * g + i % 4;
+                if (p < P.rlo || p > P.rhi)
+                    sacc[b][i] = -INFINITY;
+            }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < kNPB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            mx = fmaxf(mx, sacc[b][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const bool move = m == -INFINITY ? mx != -INFINITY : mx > kSlack + kB;
+    if (__any(move)) {
+        const float sh = move ? mx - kB : 0.0f;
+        const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-sh);
+        m = move ? mref + sh : m;
+        lsum *= alpha;
+#pragma unroll
+        for (int b = 0; b < kNPB; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                sacc[b][i] -= sh;
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                o[c][i] *= alpha;
+    }
+
+    /* weights of value k-step ks (positions 32 (ks / 2) + 16 (ks % 2) +
+       8 (e / 4) + 4 (l / 32) + e % 4), times their value scales, as two
+       planes; the sum of the weights in f32 */
+    float ls = 0.0f;
+    auto weights = [&](int ks, h8 &ph, h8 &pl) {
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) {
+            const float4 z = sop(1, ks / 2, 2 * (ks % 2) + jj);
+            const float zs[4] = {z.x, z.y, z.z, z.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float w = __builtin_amdgcn_exp2f(sacc[ks / 2][8 * (ks % 2) + 4 * jj + e]);
+                ls += w;
+                _Float16 hi, lo;
+                split_hl(w * zs[e], hi, lo);
+                ph[4 * jj + e] = hi;
+                pl[4 * jj + e] = lo;
+            }
+        }
+    };
+    h8 va[2][CT][NP];
+    h8 ph[2], pl[2];
+#pragma unroll
+    for (int c = 0; c < CT; c++)
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+            va[0][c][p] = vop(0, c, p);
+    weights(0, ph[0], pl[0]);
+#pragma unroll
+    for (int ks = 0; ks < 2 * kNPB; ks++) {
+        if (ks + 1 < 2 * kNPB) {
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+#pragma unroll
+                for (int p = 0; p < NP; p++)
+                    va[(ks + 1) & 1][c][p] = vop(ks + 1, c, p);
+            weights(ks + 1, ph[(ks + 1) & 1], pl[(ks + 1) & 1]);
+        }
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int p = 0; p < NP; p++) {
+                o[c] = mfma(va[ks & 1][c][p], ph[ks & 1], o[c]);
+                o[c] = mfma(va[ks & 1][c][p], pl[ks & 1], o[c]);
+            }
+    }
+    lsum += ls;
+}
+
+/* the kernel over the exact copy: loads and layout as prefill_dma_kernel,
+   one buffer pair holding EX planes of K and of V, and each tile's scales */
+template <int T, int D>
+__global__ __launch_bounds__((PCfg<D, false, (T == kI16 ? 2 : 1)>::W) * 64) void prefill_exact_kernel(
+    const PrefillArgs A)
+{
+    static_assert(D == 64 || D == 128 || D == 256, "rows of 8, 16 or 32 units");
+    constexpr int EX = T == kI16 ? 2 : 1, NP = EX;
+    using C = PCfg<D, false, EX>;
+    constexpr uint32_t kW = C::W, kTile = C::TILE;
+    constexpr uint32_t RB = D * 2;              /* bytes a row of a plane */
+    constexpr uint32_t UPR = RB / 16;           /* 16-byte units a row */
+    constexpr uint32_t RPI = 64 / UPR;          /* rows a load instruction */
+    constexpr uint32_t NJ = kTile / (RPI * kW); /* load instructions a wave a plane */
+    constexpr uint32_t TB = kTile * RB;         /* bytes a plane's tile */
+    constexpr int CT = D / 32, KS = D / 16;
+    constexpr int NL = 2 * NP * NJ;             /* K and V loads a wave a tile */
+    static_assert(NJ >= 1 && NJ * RPI * kW == kTile, "a tile is whole load rounds");
+    static_assert(2 * kTile <= 64 * kW, "a tile's scales are one load a wave");
+    __shared__ __attribute__((aligned(1024))) char sK0[NP * TB];
+    __shared__ __attribute__((aligned(1024))) char sV0[NP * TB];
+    __shared__ __attribute__((aligned(1024))) char sK1[NP * TB];
+    __shared__ __attribute__((aligned(1024))) char sV1[NP * TB];
+    /* a tile's scales: ks of its positions, then vs; wave w's load fills
+       floats 64 w .. 64 w + 63 (past 2 TILE they repeat) */
+    __shared__ __attribute__((aligned(16))) float sS0[64 * kW];
+    __shared__ __attribute__((aligned(16))) float sS1[64 * kW];
+
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t g = lane >> 5, l32 = lane & 31, l16 = lane & 15;
+    const PBlock P = block_of<D, false, EX>(A);
+    const SeqDesc &sq = *P.sq;
+    const uint32_t hd = A.hd;
+    const bool ring = A.ring != 0;
+    h8 qh[KS], ql[KS];
+    const float qsc = load_query_x<D>(A, P, qh, ql);
+
+    /* the copy: per KV head the positions pb .. end - 1, plane after plane */
+    const uint32_t pb = sq.c0 * kChunk, np = sq.end - pb;
+    const uint32_t rbytes = hd * 2;
+    const size_t pstride = (size_t)A.n_kv * np * rbytes;
+    const char *const kg = (const char *)sq.k, *const vg = (const char *)sq.v;
+    const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
+    const uint32_t drow = RPI * w + lane / UPR;
+    uint32_t dcol[NJ];
+#pragma unroll
+    for (int j = 0; j < (int)NJ; j++) {
+        const uint32_t unit = (lane % UPR) ^ swz<D>(drow + RPI * kW * j);
+        dcol[j] = unit * 8 < hd ? unit * 8 : 0;
+    }
+    auto tbase = [&](uint32_t tile) -> size_t {
+        return ((size_t)P.kvh * np + (tile * kTile - pb)) * rbytes;
+    };
+    auto offsets = [&](uint32_t tile, uint32_t *off) {
+        const uint32_t t0 = tile * kTile;
+#pragma unroll
+        for (int j = 0; j < (int)NJ; j++) {
+            uint32_t p = t0 + drow + RPI * kW * j;
+            p = p < P.lo_all ? P.lo_all : p > P.hi_all ? P.hi_all : p;
+            off[j] = __umul24(p - t0, rbytes) + 2 * dcol[j];
+        }
+    };
+    /* load i of a tile: K (i even) or V, plane (i / 2) / NJ, round (i / 2) % NJ */
+    auto fetch_one = [&](size_t base, const uint32_t *off, int i, char *dk, char *dv) {
+        const int r = i >> 1, p = r / (int)NJ, j = r % (int)NJ;
+        const uint32_t at = p * TB + (wu + kW * j) * 1024;
+        if (i & 1)
+            dma16(vg + base + p * pstride, off[j], dv + at);
+        else
+            dma16(kg + base + p * pstride, off[j], dk + at);
+    };
+    /* the lane's scale of tile `tile`: ks, then vs, of the position clamped
+       to the block's rows (the cache's own rows, ring-aware) */
+    const uint32_t si = (64 * w + lane) % (2 * kTile);
+    const float *const zarr = si < kTile ? sq.ks : sq.vs;
+    auto saddr = [&](uint32_t tile) -> const float * {
+        const uint32_t t0 = tile * kTile;
+        uint32_t p = t0 + si % kTile;
+        p = p < P.lo_all ? P.lo_all : p > P.hi_all ? P.hi_all : p;
+        return zarr + P.head_row + (ring ? t0 % sq.cap : t0) + (p - t0);
+    };
+    auto fetch = [&](uint32_t tile, char *dk, char *dv, float *ds) {
+        const size_t base = tbase(tile);
+        uint32_t off[NJ];
+        offsets(tile, off);
+#pragma unroll
+        for (int i = 0; i < NL; i++)
+            fetch_one(base, off, i, dk, dv);
+        dma4(saddr(tile), (char *)ds + 256 * wu);
+    };
+    uint32_t koff[KS];
+#pragma unroll
+    for (int s = 0; s < KS; s++)
+        koff[s] = l32 * RB + (((2 * s + g) ^ swz<D>(l16)) * 16);
+    const uint32_t vrow = 4 * g + (l16 >> 2);
+    const uint32_t u0 = 2 * ((lane >> 4) & 1) + ((l16 & 3) >> 1);
+    uint32_t vxo[CT], vyo[CT];
+#pragma unroll
+    for (int c = 0; c < CT; c++) {
+        vxo[c] = vrow * RB + (((4 * c + u0) ^ swz<D>(vrow)) * 16) + (l16 & 1) * 8;
+        vyo[c] = (vrow + 8) * RB + (((4 * c + u0) ^ swz<D>(vrow + 8)) * 16) + (l16 & 1) * 8;
+    }
+
+    float m = -INFINITY, lsum = 0.0f;
+    f16x o[CT];
+#pragma unroll
+    for (int c = 0; c < CT; c++)
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            o[c][i] = 0.0f;
+
+    auto step = [&](uint32_t tile, const char *ck, const char *cv, const float *cs, char *nk,
+                    char *nv, float *ns) {
+        const uint32_t nt = tile < P.tlast ? tile + 1 : tile;
+        const size_t nbase = tbase(nt);
+        uint32_t noff[NJ];
+        offsets(nt, noff);
+        const float *const nz = saddr(nt);
+        tile_pass_x<D, EX, NL>(
+            tile * kTile, P, qh, ql, qsc, m, lsum, o,
+            [&](int s, int b, int p) {
+                return *(const h8 *)(ck + p * TB + 32 * b * RB + koff[s]);
+            },
+            [&](int ks, int c, int p) {
+                const char *base = cv + p * TB + 16 * ks * RB;
+                const h4 x = lds_read_tr((const _Float16 *)(base + vxo[c]));
+                const h4 y = lds_read_tr((const _Float16 *)(base + vyo[c]));
+                return h8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+            },
+            [&](int which, int b, int j) {
+                return *(const float4 *)(cs + which * kTile + 32 * b + 8 * j + 4 * g);
+            },
+            [&](int s) {
+#pragma unroll
+                for (int i = s; i < NL; i += KS)
+                    fetch_one(nbase, noff, i, nk, nv);
+                if (s == 0)
+                    dma4(nz, (char *)ns + 256 * wu);
+            });
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (tile < P.tlast)
+            __syncthreads();
+    };
+
+    fetch(P.tfirst, sK0, sV0, sS0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (uint32_t tile = P.tfirst;; tile += 2) {
+        step(tile, sK0, sV0, sS0, sK1, sV1, sS1);
+        if (tile + 1 > P.tlast)
+            break;
+        step(tile + 1, sK1, sV1, sS1, sK0, sV0, sS0);
+        if (tile + 2 > P.tlast)
+            break;
+    }
+    finish<D>(A, P, m, lsum, o);
+}
+
+/*
+ * The exact copy of an int8 / int16 cache's rows of positions p0 .. p0 +
+ * np - 1: the integers as f16 planes whose sum is the number exactly - int8
+ * one plane, int16 two (x with its low byte cleared, and the low byte) -
+ * row kvh np + (p - p0) of each plane (the cache's row kvh cap + p, or p
+ * mod cap on a ring). A thread takes 8 numbers of one row.
  */
 template <int T>
-__global__ __launch_bounds__(256) void dequant_kernel(const DqArgs A)
+__global__ __launch_bounds__(256) void xcopy_kernel(const DqArgs A)
 {
-    using E = PElem<T>;
     const uint32_t upr = A.hd / 8;
     const uint64_t u = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (u >= (uint64_t)A.n_kv * A.np * upr)
@@ -925,13 +1375,39 @@ __global__ __launch_bounds__(256) void dequant_kernel(const DqArgs A)
     const uint32_t cu = (uint32_t)(u - row * upr);
     const uint32_t kvh = (uint32_t)(row / A.np), p = A.p0 + (uint32_t)(row % A.np);
     const size_t r = (size_t)kvh * A.cap + (A.ring ? p % A.cap : p);
-    const uint32_t off = cu * 8 * E::EB;
-    const char *kb = (const char *)A.k + r * A.hd * E::EB;
-    const char *vb = (const char *)A.v + r * A.hd * E::EB;
-    const u4 k16 = E::to_f16(E::load(kb, off), A.ks[r]);
-    const u4 v16 = E::to_f16(E::load(vb, off), A.vs[r]);
-    *(u4 *)(A.k16 + r * A.hd + cu * 8) = k16;
-    *(u4 *)(A.v16 + r * A.hd + cu * 8) = v16;
+    const size_t dst = row * A.hd + cu * 8;
+    const size_t plane = (size_t)A.n_kv * A.np * A.hd;
+    if constexpr (T == kI8) {
+        const uint2 kx = *(const uint2 *)((const char *)A.k + r * A.hd + cu * 8);
+        const uint2 vx = *(const uint2 *)((const char *)A.v + r * A.hd + cu * 8);
+        h8 kh, vh;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            kh[e] = (_Float16)(int8_t)(kx.x >> (8 * e));
+            kh[4 + e] = (_Float16)(int8_t)(kx.y >> (8 * e));
+            vh[e] = (_Float16)(int8_t)(vx.x >> (8 * e));
+            vh[4 + e] = (_Float16)(int8_t)(vx.y >> (8 * e));
+        }
+        *(h8 *)(A.k16 + dst) = kh;
+        *(h8 *)(A.v16 + dst) = vh;
+    } else {
+        const u4 kx = *(const u4 *)((const char *)A.k + 2 * (r * A.hd + cu * 8));
+        const u4 vx = *(const u4 *)((const char *)A.v + 2 * (r * A.hd + cu * 8));
+        h8 k0, k1, v0, v1;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int32_t a = (int16_t)(kx[e / 2] >> (16 * (e % 2)));
+            const int32_t b = (int16_t)(vx[e / 2] >> (16 * (e % 2)));
+            k0[e] = (_Float16)(a & ~255);
+            k1[e] = (_Float16)(a & 255);
+            v0[e] = (_Float16)(b & ~255);
+            v1[e] = (_Float16)(b & 255);
+        }
+        *(h8 *)(A.k16 + dst) = k0;
+        *(h8 *)(A.k16 + plane + dst) = k1;
+        *(h8 *)(A.v16 + dst) = v0;
+        *(h8 *)(A.v16 + plane + dst) = v1;
+    }
 }
 
 /* a group index as a type: the two key groups' loops use distinct LDS
@@ -1192,6 +1668,17 @@ __global__ __launch_bounds__(kPMergeThreads) void pmerge_kernel(const PrefillArg
 template <int T, int D>
 hipError_t launch_d(const PrefillArgs &a, hipStream_t s)
 {
+    /* int8 / int16 up to head size 256: the exact kernel only */
+    if constexpr ((T == kI8 || T == kI16) && D <= 256) {
+        constexpr int EX = T == kI16 ? 2 : 1;
+        if (a.halves || a.exact != EX)
+            return hipErrorInvalidValue;
+        hipLaunchKernelGGL((prefill_exact_kernel<T, D>), dim3(a.n_wg),
+                           dim3(PCfg<D, false, EX>::W * 64), 0, s, a);
+        return hipGetLastError();
+    }
+    if (a.exact)
+        return hipErrorInvalidValue;
     if constexpr (T == kF16 && D == 128) {
         if (a.halves) {
             hipLaunchKernelGGL((prefill_half_kernel<D>), dim3(a.n_wg), dim3((PCfg<D, true>::W) * 64), 0, s, a);
@@ -1202,7 +1689,7 @@ hipError_t launch_d(const PrefillArgs &a, hipStream_t s)
         return hipErrorInvalidValue;
     if constexpr (T == kF16 && (D == 64 || D == 128 || D == 256))
         hipLaunchKernelGGL((prefill_dma_kernel<D>), dim3(a.n_wg), dim3(PCfg<D>::W * 64), 0, s, a);
-    else
+    else if constexpr (D > 256)
         hipLaunchKernelGGL((prefill_kernel<T, D>), dim3(a.n_wg), dim3(PCfg<D>::W * 64), 0, s, a);
     return hipGetLastError();
 }
@@ -1229,23 +1716,27 @@ int prefill_supported(int kv, uint32_t hd)
            hd <= 512;
 }
 
-uint32_t prefill_tile(uint32_t hd, bool halves)
+uint32_t prefill_tile(uint32_t hd, bool halves, int exact)
 {
     if (halves)
         return PCfg<128, true>::TILE;
+    if (exact == 1)
+        return hd > 128 ? PCfg<256, false, 1>::TILE : PCfg<128, false, 1>::TILE;
+    if (exact == 2)
+        return hd > 128 ? PCfg<256, false, 2>::TILE : PCfg<128, false, 2>::TILE;
     return hd > 256 ? PCfg<512>::TILE : hd > 128 ? PCfg<256>::TILE : PCfg<128>::TILE;
 }
 
-hipError_t launch_dequant(int kv, const DqArgs &a, hipStream_t s)
+hipError_t launch_xcopy(int kv, const DqArgs &a, hipStream_t s)
 {
     const uint64_t n = (uint64_t)a.n_kv * a.np * (a.hd / 8);
     if (n == 0 || a.hd % 8)
         return hipErrorInvalidValue;
     const dim3 grid((uint32_t)((n + 255) / 256));
     if (kv == kI8)
-        hipLaunchKernelGGL(dequant_kernel<kI8>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(xcopy_kernel<kI8>, grid, dim3(256), 0, s, a);
     else if (kv == kI16)
-        hipLaunchKernelGGL(dequant_kernel<kI16>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(xcopy_kernel<kI16>, grid, dim3(256), 0, s, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -1263,12 +1754,14 @@ hipError_t launch_prefill_merge(const PrefillArgs &a, uint32_t n_wg, hipStream_t
     return hipGetLastError();
 }
 
-uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd, bool halves)
+uint32_t prefill_row_blocks(uint32_t n, uint32_t group, uint32_t hd, bool halves, int exact)
 {
     /* a workgroup takes PCfg::BLOCK of a KV head's n x group rows */
     const uint64_t block = halves ? PCfg<128, true>::BLOCK
                          : hd > 256 ? PCfg<512>::BLOCK
-                         : hd > 128 ? PCfg<256>::BLOCK : PCfg<128>::BLOCK;
+                         : hd > 128 ? PCfg<256>::BLOCK
+                         : exact == 2 && hd > 64 ? PCfg<128, false, 2>::BLOCK
+                         : exact == 2 ? PCfg<64, false, 2>::BLOCK : PCfg<128>::BLOCK;
     return (uint32_t)(((uint64_t)n * group + block - 1) / block);
 }
 

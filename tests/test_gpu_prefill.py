@@ -16,8 +16,9 @@ import pytest
 import torch
 
 import janas_amd
-from attn_helpers import (KV_F16, KV_F32, TOL_F16_ABS, TOL_F32_REL, abs_err,
-                          cache, config, oracle_out, rel_err, threads, within)
+from attn_helpers import (KV_F16, KV_F32, TOL_F16_ABS, TOL_F32_REL,
+                          TOL_FLOAT_ABS, abs_err, cache, config, oracle_out,
+                          rel_err, threads, within)
 from cases import normal
 from janas_amd import Attention
 from oracle import orc
@@ -373,6 +374,14 @@ def quantized(seed, n_kv, cap, hd, wide):
     return q, z
 
 
+def quantized_bar(hd):
+    """int8 / int16 caches up to head size 256 take the exact kernel (the
+    cached integers exact, the query and the weights as two f16 planes):
+    the reference's own FLOAT bar (test_attention.c:146). Above 256 the
+    register-staged kernel dequantizes rows into f16: the f16 bar."""
+    return TOL_FLOAT_ABS if hd <= 256 else TOL_F16_ABS
+
+
 @pytest.mark.parametrize("wide", [False, True])
 @pytest.mark.parametrize("geom", [dict(n_head=32, n_kv=8, hd=128, cap=1024,
                                        n=1024, pos0=0),
@@ -383,13 +392,15 @@ def quantized(seed, n_kv, cap, hd, wide):
                                        ring=True),
                                   dict(n_head=16, n_kv=2, hd=256, cap=800,
                                        n=500, pos0=100),
+                                  dict(n_head=6, n_kv=3, hd=200, cap=700,
+                                       n=90, pos0=0),
                                   dict(n_head=16, n_kv=2, hd=512, cap=900,
                                        n=300, pos0=400, window=1024)])
 def test_prefill_quantized_cache(gpu, wide, geom):
     """int8 / int16 caches with their scales (the engine's own format) on
-    the MFMA path: rows dequantized into f16 as tiles are staged, or, for
-    prompts of 256 tokens or more at head sizes up to 256, into an f16 copy
-    first; the bar is the f16 one."""
+    the MFMA path: up to head size 256 the exact kernel over a copy of the
+    visible rows as f16 planes, within the reference's FLOAT bar; at 512
+    the rows dequantized into f16 as tiles are staged, within the f16 bar."""
     h, kvh, hd, cap = geom["n_head"], geom["n_kv"], geom["hd"], geom["cap"]
     n, pos0 = geom["n"], geom["pos0"]
     k, ks = quantized(400 + hd, kvh, cap, hd, wide)
@@ -408,7 +419,7 @@ def test_prefill_quantized_cache(gpu, wide, geom):
                             q=to_dev(q, gpu), out=out, cap=cap, n=n,
                             pos0=pos0)], path="prefill")
         torch.cuda.synchronize()
-        # the prefill path (and, for long prompts, its f16 copy pass), not
+        # the prefill path (and, up to head size 256, its copy pass), not
         # the split path
         prof = a.prof_read()
         assert prof["prefill"][0] >= 1 and prof["split"][0] == 0
@@ -417,18 +428,18 @@ def test_prefill_quantized_cache(gpu, wide, geom):
                   ring=geom.get("ring", False), threads=threads(), block=64)
     err = abs_err(out.cpu().numpy(), ref)
     print(f"{geom} wide={wide}: max abs err {err:.2e}")
-    assert within(err, TOL_F16_ABS, "vs oracle")
+    assert within(err, quantized_bar(hd), "vs oracle")
 
 
-@pytest.mark.parametrize("hd", [128, 64])
+@pytest.mark.parametrize("hd", [128, 64, 256])
 @pytest.mark.parametrize("wide", [False, True])
-def test_prefill_quantized_long_prompt_f16_copy(gpu, wide, hd):
-    """A long int8 / int16 prompt runs the f16 kernels over an f16 copy of
-    its rows (f16(x * scale), the numbers the register-staged kernel
-    stages): bitwise equal to the allocation-free entry point, which keeps
-    the register-staged kernel, and within the bar of the restatement.
-    Head size 64 takes the DMA kernel's 128-byte rows."""
-    h, kvh, n, pos0 = 32, 8, 2048, 0
+def test_prefill_quantized_long_prompt_exact(gpu, wide, hd):
+    """A long int8 / int16 prompt through janas_attn_run_dev (the engine's
+    route for calls of more than 64 tokens) takes the exact kernel over a
+    copy of its rows; the allocation-free entry point, whose copy and
+    partials sit in the device's fixed array, gives the same bits. Both
+    within the reference's FLOAT bar of the restatement."""
+    h, kvh, n, pos0 = (32, 8, 2048, 0) if hd <= 128 else (16, 2, 1536, 0)
     k, ks = quantized(9100 + wide, kvh, n, hd, wide)
     v, vs = quantized(9102 + wide, kvh, n, hd, wide)
     q = normal(9104, n * h * hd).reshape(n, h, hd)
@@ -436,18 +447,53 @@ def test_prefill_quantized_long_prompt_f16_copy(gpu, wide, hd):
     d = dict(k=to_dev(k, gpu), v=to_dev(v, gpu), ks=to_dev(ks, gpu),
              vs=to_dev(vs, gpu), q=to_dev(q, gpu), cap=n, n=n, pos0=pos0)
     outs = []
-    with Attention(h, kvh, hd, n) as a:
-        for path in ("prefill", "noalloc"):
+    with Attention(h, kvh, hd, n, 1, janas_amd.FLOAT) as a:
+        for path in ("auto", "noalloc"):
             dd = dict(d, out=torch.full(d["q"].shape, float("nan"), device=gpu))
+            a.prof_enable(True)
             a.run_dev(kv, [dd], path=path)
             torch.cuda.synchronize()
+            prof = a.prof_read()
+            if path == "auto":
+                assert prof["prefill"][0] >= 1 and prof["split"][0] == 0
             outs.append(dd["out"].cpu().numpy())
     assert np.array_equal(outs[0].view(np.int32), outs[1].view(np.int32))
     ref = orc.run(q.astype(np.float32), k, v, ks, vs, n_head=h, n_kv=kvh,
                   hd=hd, pos0=pos0, kv=kv, threads=threads(), block=64)
     err = abs_err(outs[0], ref)
-    print(f"f16 copy {'int16' if wide else 'int8'} hd {hd}: max abs err {err:.2e}")
-    assert within(err, TOL_F16_ABS, "vs oracle")
+    print(f"exact {'int16' if wide else 'int8'} hd {hd}: max abs err {err:.2e}")
+    assert within(err, TOL_FLOAT_ABS, "vs oracle")
+
+
+@pytest.mark.parametrize("wide", [False, True])
+def test_prefill_quantized_8k(gpu, wide):
+    """The benched 8k prompt (32 / 8 / 128, one call) over the engine's own
+    int8 / int16 cache, checked against the restatement over row blocks of
+    512 tokens at the start, the middle and the end, at the reference's
+    FLOAT bar."""
+    h, kvh, hd, L, step = 32, 8, 128, 8192, 512
+    k, ks = quantized(9200 + wide, kvh, L, hd, wide)
+    v, vs = quantized(9202 + wide, kvh, L, hd, wide)
+    q = normal(9204, L * h * hd).reshape(L, h, hd)
+    kv = janas_amd.KV_I16 if wide else janas_amd.KV_I8
+    out = torch.full((L, h, hd), float("nan"), device=gpu)
+    with Attention(h, kvh, hd, L, 1, janas_amd.FLOAT) as a:
+        a.prof_enable(True)
+        a.run_dev(kv, [dict(k=to_dev(k, gpu), v=to_dev(v, gpu),
+                            ks=to_dev(ks, gpu), vs=to_dev(vs, gpu),
+                            q=to_dev(q, gpu), out=out, cap=L, n=L, pos0=0)])
+        torch.cuda.synchronize()
+        prof = a.prof_read()
+        assert prof["prefill"][0] >= 1 and prof["split"][0] == 0
+    o = out.cpu().numpy()
+    worst = 0.0
+    for c in (0, 1, 8, 15):
+        p0 = c * step
+        ref = orc.run(q[p0:p0 + step], k, v, ks, vs, n_head=h, n_kv=kvh,
+                      hd=hd, pos0=p0, kv=kv, threads=threads(), block=64)
+        worst = max(worst, abs_err(o[p0:p0 + step], ref))
+    print(f"8k {'int16' if wide else 'int8'}: max abs err {worst:.2e}")
+    assert within(worst, TOL_FLOAT_ABS, "blocks 0 1 8 15 vs oracle")
 
 
 def test_prefill_refuses_what_it_has_no_kernel_for(gpu):
