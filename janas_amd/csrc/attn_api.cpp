@@ -489,6 +489,7 @@ float time_way(janas_attn *a, int way, const janas_attn_seq &s, hipEvent_t e0, h
 void calibrate(janas_attn *a)
 {
     a->calibrated = 1;
+    const uint64_t rows0 = a->part_rows;
     a->from16[0] = a->from16[1] = UINT32_MAX;
     {
         std::lock_guard<std::mutex> lk(g_calib_mu);
@@ -507,6 +508,9 @@ void calibrate(janas_attn *a)
     void *k = nullptr, *v = nullptr, *ks = nullptr, *vs = nullptr, *q = nullptr, *out = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     const int keep = a->scores;
+    /* the measurement's own launches are not the caller's to count */
+    const int prof = a->prof;
+    a->prof = 0;
     bool ok = hipMalloc(&k, cells * a->hd) == hipSuccess &&
               hipMalloc(&v, cells * a->hd) == hipSuccess &&
               hipMalloc(&ks, cells * sizeof(float)) == hipSuccess &&
@@ -570,6 +574,16 @@ void calibrate(janas_attn *a)
     if (e1)
         (void)hipEventDestroy(e1);
     a->scores = keep;
+    a->prof = prof;
+    /* the measurement's partials are not kept: back to the size before */
+    if (a->part_rows > rows0) {
+        (void)hipFree(a->part_ml);
+        (void)hipFree(a->part_acc);
+        a->part_ml = a->part_acc = nullptr;
+        a->part_rows = 0;
+        if (rows0 && ensure_part(a, rows0, a->stream) != JANAS_ATTN_OK)
+            (void)hipGetLastError();
+    }
     if (!ok)
         return;
     std::lock_guard<std::mutex> lk(g_calib_mu);
@@ -590,23 +604,31 @@ void choose_way(janas_attn *a, int kv, uint32_t n, uint32_t pos0)
     a->scores = pos0 >= a->from16[n > 1] ? JANAS_ATTN_INT16 : JANAS_ATTN_FLOAT;
 }
 
-/* The same choice for a Part 2 call of one sequence on the split path,
-   unless the stream is being captured into a graph (the first call's
-   measurement allocates and synchronizes; a captured call keeps the way
-   last resolved) */
+/* The same choice for a Part 2 call, of any length and any number of
+   sequences: the way is measured at the first call that is not being
+   captured into a graph (the measurement allocates and synchronizes) and
+   is not the allocation-free entry point's (fixed); until it is measured,
+   AUTO computes the FLOAT way. A call of n tokens at pos0 takes INT16 from
+   from16[n > 1] on, as a call of the reference's (a prompt longer than a
+   block follows the block's rule); a call of several sequences only when
+   each of them would. So the way of a call never depends on what an
+   earlier call was, except through the one measurement. */
 void choose_way_dev(janas_attn *a, int kv, const janas_attn_seq *seqs, uint32_t n_seqs,
-                    hipStream_t st)
+                    hipStream_t st, bool fixed)
 {
-    if (n_seqs != 1 || seqs[0].n > JANAS_ATTN_MAX_BLOCK)
+    if (!a->scores_auto || a->kv16 || kv != kI8 || a->hd % 16)
         return;
-    if (!a->calibrated) {
+    if (!a->calibrated && !fixed) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess)
             (void)hipGetLastError();
-            return;
-        }
+        else if (cs == hipStreamCaptureStatusNone)
+            calibrate(a);
     }
-    choose_way(a, kv, seqs[0].n, seqs[0].pos0);
+    bool int16 = a->calibrated != 0;
+    for (uint32_t i = 0; i < n_seqs; i++)
+        int16 = int16 && seqs[i].pos0 >= a->from16[seqs[i].n > 1];
+    a->scores = int16 ? JANAS_ATTN_INT16 : JANAS_ATTN_FLOAT;
 }
 
 /* Key segments for a prefill sequence whose row blocks alone would leave
@@ -1254,7 +1276,7 @@ extern "C" int janas_attn_run_dev_split(struct janas_attn *a, int kv_type,
     if (rc)
         return rc;
     hipStream_t st = stream ? (hipStream_t)stream : a->stream;
-    choose_way_dev(a, kv_type, seqs, n_seqs, st);
+    choose_way_dev(a, kv_type, seqs, n_seqs, st, false);
     rc = run_split(a, kv_type, gate_mode, seqs, n_seqs, st);
     return note(a, rc);
 }
@@ -1283,8 +1305,7 @@ int run_dev(janas_attn *a, int kv_type, int gate_mode, const janas_attn_seq *seq
     if (rc)
         return rc;
     hipStream_t st = stream ? (hipStream_t)stream : a->stream;
-    if (!fixed)
-        choose_way_dev(a, kv_type, seqs, n_seqs, st);
+    choose_way_dev(a, kv_type, seqs, n_seqs, st, fixed);
     /* blocks of up to JANAS_ATTN_MAX_BLOCK tokens keep the split-KV
        chunking of janas_attn_run; longer prompts take the prefill tiles */
     bool any_long = false;

@@ -243,7 +243,11 @@ constexpr float kCut2 = -115.41560327111707f;
    own, bit for bit ---- */
 
 /* janas_exp_det (vmath.h:36-52): e^x by the Cephes expf polynomial on
-   x - n ln 2, ln 2 in two parts, 2^n put into the exponent */
+   x - n ln 2, ln 2 in two parts, 2^n put into the exponent. A restatement
+   of the reference's function, step for step and with its constants, so
+   that the INT16 way's weights are its bits: from Janas-LLM
+   (prabanta-dev/janas, src/llm/vmath.h), GPL-3.0-or-later; the
+   polynomial is Cephes' expf (Stephen L. Moshier). */
 __device__ __forceinline__ float exp_det(float x)
 {
 #pragma clang fp contract(off)

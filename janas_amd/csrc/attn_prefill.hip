@@ -303,7 +303,10 @@ __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
     P.rj = (P.rok ? r : r0) / G;
     P.rh = kvh * G + (P.rok ? r : r0) % G;
     P.rlo = P.rok && !empty ? row_lo(A, sq.pos0 + P.rj) : 1;
-    P.rhi = P.rok && !empty ? (sq.last ? sq.last[P.rj] : sq.pos0 + P.rj) : 0;
+    /* set_last's bound, clamped to the call's end as the split path
+       clamps it (a last[] past last_max sees up to last_max) */
+    const uint32_t rl = sq.last ? min(sq.last[P.rj], sq.end - 1) : sq.pos0 + P.rj;
+    P.rhi = P.rok && !empty ? rl : 0;
     return P;
 }
 

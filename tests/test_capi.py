@@ -2,6 +2,8 @@
 header declares, and its host-only entry points keep the reference's
 meaning (attention.c:984-992, :1048-1054). No GPU call is made."""
 import ctypes
+import os
+import subprocess
 
 import pytest
 
@@ -95,3 +97,57 @@ def test_status_of_no_instance_is_einval():
     L.janas_attn_clear_status(None)
     L.janas_attn_set_abort(None, 0)
 
+
+
+REF_SRC = "/root/reference/src"
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(REF_SRC, "llm", "attention.h")),
+                    reason="the reference's sources are not here (only in the "
+                           "build container)")
+def test_reference_header_caller_links_unchanged(tmp_path):
+    """A C caller written against the reference's own header
+    (src/llm/attention.h, as model_attn.c includes it) compiles and links
+    against libjanas_attn.so with no change, every one of the twelve entry
+    points bound; run, it calls the two that need no device and checks
+    them against the reference's formulas (attention.c:984-992,
+    :1048-1054)."""
+    src = tmp_path / "caller.c"
+    src.write_text(r'''
+#include <stdio.h>
+#include "llm/attention.h"
+
+/* every entry point model_attn.c and model_assist.c call, bound */
+static void *bound[] = {
+    (void *)janas_attn_part_bytes, (void *)janas_attn_create,
+    (void *)janas_attn_destroy, (void *)janas_attn_set_scale,
+    (void *)janas_attn_set_window, (void *)janas_attn_set_kv16,
+    (void *)janas_attn_set_ring, (void *)janas_attn_ring_positions,
+    (void *)janas_attn_set_last, (void *)janas_attn_scores_mode,
+    (void *)janas_attn_scores_auto, (void *)janas_attn_run,
+};
+
+int main(void)
+{
+    for (unsigned i = 0; i < sizeof bound / sizeof bound[0]; i++)
+        if (!bound[i])
+            return 2;
+    size_t pb = janas_attn_part_bytes(32, 8, 128, 1024);
+    uint32_t rp = janas_attn_ring_positions(4096, 64);
+    printf("%zu %u\n", pb, rp);
+    return 0;
+}
+''')
+    exe = tmp_path / "caller"
+    libdir = os.path.dirname(janas_amd.attention.LIB_PATH)
+    cmd = ["gcc", "-std=gnu11", "-O1", "-I", REF_SRC, "-I",
+           os.path.join(os.path.dirname(REF_SRC), "include"), str(src),
+           "-o", str(exe), "-L", libdir, "-ljanas_attn",
+           f"-Wl,-rpath,{libdir}"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    pb, rp = (int(x) for x in r.stdout.split())
+    assert pb == 8 * 4 * janas_amd.MAX_BLOCK * 4 * 130 * 4
+    assert rp == (4096 + 64 + 256 + 255) // 256 * 256

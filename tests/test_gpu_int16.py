@@ -349,3 +349,46 @@ def test_auto_measured_way(gpu, monkeypatch):
     with Attention(h, kvh, 128, L, 1, janas_amd.AUTO) as a:
         a.set_kv16(True)
         assert a.scores_mode() == janas_amd.FLOAT
+
+
+@pytest.mark.parametrize("n_ctx,n", [(32768, 2048), (20000, 512)])
+def test_auto_long_prompt_first_call(gpu, monkeypatch, n_ctx, n):
+    """A fresh AUTO instance over an int8 cache past 16384 positions (INT16
+    at create, as the reference's scores_choice) whose first call is a long
+    prompt through janas_attn_run_dev: the call measures the way first and
+    follows the reference's block rule (INT16 only from from16[1], which
+    the device never measures below FLOAT's time), so the prompt takes the
+    exact prefill kernel, bit for bit the explicit prefill path's output,
+    and the allocation-free entry point on a fresh instance (which never
+    measures and computes FLOAT until measured) gives the same bits. The
+    output is within the reference's FLOAT bar of the restatement."""
+    monkeypatch.delenv("JANAS_ATTN", raising=False)
+    h, kvh, hd = 32, 8, 128
+    k, ks = int8_cache(611, kvh, n, hd)
+    v, vs = int8_cache(612, kvh, n, hd)
+    q = normal(613, n * h * hd).reshape(n, h, hd)
+    kd, vd, ksd, vsd, qd = (to_dev(x, gpu) for x in (k, v, ks, vs, q))
+
+    def call(path, scores=janas_amd.AUTO, prof=False):
+        out = torch.full((n, h, hd), float("nan"), device=gpu)
+        with Attention(h, kvh, hd, n_ctx, 1, scores) as a:
+            assert scores != janas_amd.AUTO or a.scores_mode() == janas_amd.INT16
+            a.prof_enable(prof)
+            a.run_dev(janas_amd.KV_I8, [dict(k=kd, v=vd, ks=ksd, vs=vsd, q=qd,
+                                              out=out, cap=n, n=n, pos0=0)],
+                      path=path)
+            torch.cuda.synchronize()
+            p = a.prof_read() if prof else None
+            assert a.status() == 0
+        return out.cpu().numpy(), p
+
+    first, prof = call("auto", prof=True)
+    assert prof["prefill"][0] >= 1 and prof["split"][0] == 0, prof
+    explicit, _ = call("prefill", janas_amd.FLOAT)
+    noalloc, _ = call("noalloc")
+    assert np.array_equal(first.view(np.int32), explicit.view(np.int32))
+    assert np.array_equal(first.view(np.int32), noalloc.view(np.int32))
+    ref = orc.run(q, k, v, ks, vs, n_head=h, n_kv=kvh, hd=hd, pos0=0,
+                  kv=orc.KV_I8, threads=threads(), block=64)
+    assert within(abs_err(first, ref), TOL_FLOAT_ABS,
+                  f"AUTO first call, {n} tokens")

@@ -517,3 +517,44 @@ def test_prefill_refuses_what_it_has_no_kernel_for(gpu):
     ref = orc.run(q, k, v, None, None, n_head=h, n_kv=kvh, hd=hd, pos0=0,
                   kv=KV_F32, threads=threads(), block=64)
     assert within(rel_err(d["out"].cpu().numpy(), ref), TOL_F32_REL, "rel_err(d['out'].cpu().numpy(), ref)")
+
+
+@pytest.mark.parametrize("kv", [KV_F16, janas_amd.KV_I8])
+@pytest.mark.parametrize("path,n", [("split", 40), ("prefill", 200)])
+def test_last_past_last_max_is_clamped(gpu, kv, path, n):
+    """set_last entries past the call's last_max see up to last_max, on the
+    split path and on the prefill path (f16 and the exact int8 kernel)
+    alike: the same bits as the call with those entries clamped, and within
+    the bar of the restatement given the clamped entries."""
+    h, kvh, hd, cap, pos0 = 8, 2, 128, 600, 150
+    last_max = pos0 + n - 1 + 20
+    last = np.arange(pos0, pos0 + n, dtype=np.int64)
+    last[n // 3: 2 * n // 3] = pos0 + n - 1 + 15      # a span, inside
+    last[2 * n // 3:] = last_max + 37                  # past last_max
+    clamped = np.minimum(last, last_max)
+    if kv == KV_F16:
+        k = cache(321, kvh, cap, hd, np.float16)
+        v = cache(322, kvh, cap, hd, np.float16)
+        ks = vs = None
+    else:
+        k, ks = quantized(321, kvh, cap, hd, False)
+        v, vs = quantized(322, kvh, cap, hd, False)
+    q = normal(323, n * h * hd).reshape(n, h, hd)
+    outs = []
+    with Attention(h, kvh, hd, cap, 1, janas_amd.FLOAT) as a:
+        for lst in (last, clamped):
+            d = dict(k=to_dev(k, gpu), v=to_dev(v, gpu), q=to_dev(q, gpu),
+                     out=torch.full((n, h, hd), float("nan"), device=gpu),
+                     cap=cap, n=n, pos0=pos0, last_max=last_max,
+                     last=to_dev(lst.astype(np.uint32).view(np.int32), gpu))
+            if ks is not None:
+                d.update(ks=to_dev(ks, gpu), vs=to_dev(vs, gpu))
+            a.run_dev(kv, [d], path=path)
+            torch.cuda.synchronize()
+            outs.append(d["out"].cpu().numpy())
+    assert np.array_equal(outs[0].view(np.int32), outs[1].view(np.int32))
+    ref = orc.run(q, k, v, ks, vs, n_head=h, n_kv=kvh, hd=hd, pos0=pos0,
+                  kv=kv, last=clamped.astype(np.uint32), threads=threads(),
+                  block=64)
+    bar = TOL_F16_ABS if (kv == KV_F16 and path == "prefill") else TOL_FLOAT_ABS
+    assert within(abs_err(outs[0], ref), bar, f"{path} clamped last[]")
