@@ -205,7 +205,7 @@ def cpu_prefill_baseline(w, block=64, every=8):
                       f"the work (flops) of the calls: {t_prompt:.2f} s"}
 
 
-NCOPY = 6  # 6 caches of 67 MB: more than the 256 MB infinity cache
+NCOPY = 9  # 9 caches of 67 MB: more than twice the 256 MB infinity cache
 
 
 def bench_decode(torch, jm, w, steps, warmup, kv=None, ncopy=NCOPY,
@@ -258,8 +258,10 @@ def bench_decode(torch, jm, w, steps, warmup, kv=None, ncopy=NCOPY,
         return e0.elapsed_time(e1) / n, time.perf_counter() - t0
 
     ms, wall = timed(calls("split"), steps)
-    split_ms, _ = timed(calls("split-kernel"), steps)
-    merge_ms, _ = timed(calls("merge-kernel"), steps)
+    # each kernel alone: at least 500 launches (a 4 us kernel timed over a
+    # handful of launches is mostly the events' own granularity)
+    split_ms, _ = timed(calls("split-kernel"), max(steps, 500))
+    merge_ms, _ = timed(calls("merge-kernel"), max(steps, 500))
     a.close()
     return ms, wall, split_ms, merge_ms
 
@@ -340,8 +342,11 @@ def configs_leg(torch, jm, steps=200, warmup=20):
     """BASELINE configs 1, 2, 3, 5a and 5b (synthetic N(0, 1), seeded):
     one call (5b: the 16 chunk calls) through janas_attn_run_dev, on a
     stream of its own. Decode-like configs rotate over enough cache copies
-    to exceed the 256 MB infinity cache (config 1's 8 MB is launch-bound
-    by design and is not rotated)."""
+    to exceed twice the 256 MB infinity cache (config 1's 8 MB is
+    launch-bound by design and is not rotated). Also the drop-in's own
+    prefill shape: a 64-token block at 4096 positions, the calls
+    model_attn.c:343-353 makes, through janas_attn_run over an int8 cache
+    and through janas_attn_run_dev over f16."""
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream()
     h, kvh, hd = 32, 8, 128
@@ -381,11 +386,11 @@ def configs_leg(torch, jm, steps=200, warmup=20):
                 "f32 K/V and q (launch-bound)")
     rng = np.random.default_rng(SEED + 23)
     lens = [int(x) for x in rng.integers(512, 8193, 8)]
-    decode_like("3", rng, jm.KV_F16, np.float16, lens, 1, 2,
+    decode_like("3", rng, jm.KV_F16, np.float16, lens, 1, 5,
                 f"ragged decode, 8 sequences of {lens} positions, 32 / 8 "
                 "heads, head_dim 128, f16 K/V, f32 q, one call")
     rng = np.random.default_rng(SEED + 25)
-    decode_like("5a", rng, jm.KV_F16, np.float16, [8200], 8, 8,
+    decode_like("5a", rng, jm.KV_F16, np.float16, [8200], 8, 16,
                 "verify: 8 drafts at positions 8192..8199 over the cache, "
                 "32 / 8 heads, head_dim 128, f16 K/V, f32 q")
 
@@ -415,6 +420,50 @@ def configs_leg(torch, jm, steps=200, warmup=20):
                  "chunked prefill: an 8192-token prompt as 16 calls of 512 "
                  "(pos0 = 512 c) over the growing cache, 32 / 8 heads, "
                  "head_dim 128, f16 K/V, f32 q")
+
+    # the drop-in's prefill: one 64-token block at positions 4096..4159
+    L, n, p0 = 4160, 64, 4096
+    rng = np.random.default_rng(SEED + 27)
+    kf = normal(rng, (kvh, L, hd), np.float32)
+    vf = normal(rng, (kvh, L, hd), np.float32)
+    q = dev_t(normal(rng, (n, h, hd), np.float32))
+    out = torch.empty_like(q)
+    fl = prefill_flops(hd, h, p0, n)
+    k8, ks8 = quantized(kf, np.int8)
+    v8, vs8 = quantized(vf, np.int8)
+    k8, ks8, v8, vs8 = (dev_t(x) for x in (k8, ks8, v8, vs8))
+    a = jm.Attention(h, kvh, hd, L, 1, jm.FLOAT)
+    # janas_attn_run is synchronous on the instance's own stream: the time
+    # a caller waits, by the host clock, over back-to-back calls
+    for _ in range(warmup):
+        a.run(q, k8, ks8, v8, vs8, n, p0, out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        a.run(q, k8, ks8, v8, vs8, n, p0, out)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    a.close()
+    res["block64-dropin-int8"] = {
+        "workload": "janas_attn_run (the drop-in), 64 tokens at positions "
+                    "4096..4159, 32 / 8 heads, head_dim 128, int8 K/V with "
+                    "per-row scales, FLOAT scores, device pointers; host "
+                    "clock around each synchronous call",
+        "ms": round(ms, 5), "value": round(fl / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s", "flops": fl, "bound": "mfma",
+        "frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+    k16, v16 = dev_t(kf.astype(np.float16)), dev_t(vf.astype(np.float16))
+    a = jm.Attention(h, kvh, hd, L)
+    fn = a.prepare(jm.KV_F16, [dict(k=k16, v=v16, q=q, out=out, cap=L, n=n,
+                                    pos0=p0)], stream=stream.cuda_stream)
+    ms = _timed(torch, [fn], steps, warmup, stream)
+    a.close()
+    res["block64-f16"] = {
+        "workload": "janas_attn_run_dev, one 64-token block at positions "
+                    "4096..4159 (split path: a block equals its tokens), "
+                    "32 / 8 heads, head_dim 128, f16 K/V, f32 q",
+        "ms": round(ms, 5), "value": round(fl / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s", "flops": fl, "bound": "mfma",
+        "frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
     return res
 
 
@@ -432,11 +481,11 @@ def bench_copy(torch, steps):
 
 
 def wide_leg(torch, jm, steps, warmup):
-    """The head_dim 512 int16 decode (wide kernel + merge), 3 cache copies
+    """The head_dim 512 int16 decode (wide kernel + merge), 5 cache copies
     of 134 MB so none stays in the infinity cache."""
     w = wide_workload()
     ms, _, split_ms, merge_ms = bench_decode(torch, jm, w, steps, warmup,
-                                             kv=jm.KV_I16, ncopy=3)
+                                             kv=jm.KV_I16, ncopy=5)
     kv_bytes = 2 * w["kvh"] * w["L"] * w["hd"] * 2 + 2 * w["kvh"] * w["L"] * 4
     achieved = kv_bytes / (split_ms * 1e-3) / 1e9
     return {
@@ -466,9 +515,9 @@ def int_leg(torch, jm, steps, warmup, prefill_steps=5):
     rows quantized to int8 and to int16."""
     res = {}
     for name, dtype, kv, ncopy, scores in (
-            ("4-int8", np.int8, jm.KV_I8, 8, jm.FLOAT),
-            ("4-int8-int16", np.int8, jm.KV_I8, 8, jm.INT16),
-            ("4-int16", np.int16, jm.KV_I16, 5, jm.FLOAT)):
+            ("4-int8", np.int8, jm.KV_I8, 16, jm.FLOAT),
+            ("4-int8-int16", np.int8, jm.KV_I8, 16, jm.INT16),
+            ("4-int16", np.int16, jm.KV_I16, 8, jm.FLOAT)):
         w = int_decode_workload(dtype)
         ms, _, split_ms, merge_ms = bench_decode(torch, jm, w, steps, warmup,
                                                  kv=kv, ncopy=ncopy,
