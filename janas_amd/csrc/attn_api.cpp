@@ -11,8 +11,11 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <sys/stat.h>
+
 #include <algorithm>
 #include <mutex>
+#include <string>
 #include <vector>
 
 #include <hip/hip_runtime.h>
@@ -447,10 +450,14 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
  * 2048, ... up to 65536 and a 64-token block up to 16384 are timed both
  * ways on the device (the faster of three calls each, HIP events on the
  * instance's stream); INT16 is taken from the first position from which it
- * wins at every longer one. The reference keeps its measurements in a file
- * under its cache directory; here they are kept for the process, by device
- * and geometry. On gfx950 INT16 costs 5-8 % more than FLOAT at every
- * length, so AUTO measures to FLOAT.
+ * wins at every longer one. As the reference keeps its measurements in
+ * attn.txt under its cache directory (attention.c:1118-1164, tuner.c:
+ * 343-365), these are kept for the process and in attn_gpu.txt there
+ * ($XDG_CACHE_HOME/janas, else ~/.cache/janas): one line a measurement,
+ * "key from16[0] from16[1]", the key naming the device (its name,
+ * architecture and compute units) and the geometry, so every later process
+ * on the same kind of device takes it without measuring. On gfx950 INT16
+ * costs 5-8 % more than FLOAT at every length, so AUTO measures to FLOAT.
  */
 struct Calib {
     int dev, ring;
@@ -464,6 +471,73 @@ bool calib_same(const Calib &c, const janas_attn *a)
 {
     return c.dev == a->dev && c.ring == a->ring && c.n_head == a->n_head && c.n_kv == a->n_kv &&
            c.hd == a->hd && c.window == a->window && c.n_ctx == a->n_ctx;
+}
+
+/* the measurement's key: device, then geometry (no blanks) */
+std::string calib_key(const janas_attn *a)
+{
+    hipDeviceProp_t pr;
+    std::string dev = "gpu";
+    if (hipGetDeviceProperties(&pr, a->dev) == hipSuccess)
+        dev = std::string(pr.name) + "|" + pr.gcnArchName + "|" +
+              std::to_string(pr.multiProcessorCount);
+    else
+        (void)hipGetLastError();
+    for (char &c : dev)
+        if (c == ' ' || c == '\t' || c == '\n')
+            c = '_';
+    char geo[160];
+    snprintf(geo, sizeof geo, "|%d|%u/%u/%u|%u|%u", a->ring, a->n_head, a->n_kv, a->hd,
+             a->window, a->n_ctx);
+    return dev + geo;
+}
+
+/* the cache directory's file (tuner.c:343-365's directory), made if
+   `create`; empty when there is no home */
+std::string calib_path(bool create)
+{
+    const char *xdg = getenv("XDG_CACHE_HOME"), *home = getenv("HOME");
+    std::string dir = xdg && *xdg ? std::string(xdg) + "/janas"
+                    : home        ? std::string(home) + "/.cache/janas"
+                                  : std::string();
+    if (dir.empty())
+        return dir;
+    if (create)
+        for (size_t i = 1; i <= dir.size(); i++)
+            if (i == dir.size() || dir[i] == '/')
+                (void)mkdir(dir.substr(0, i).c_str(), 0755);
+    return dir + "/attn_gpu.txt";
+}
+
+/* the last line for `key` (later lines win, as appended), or false */
+bool calib_load(const std::string &key, uint32_t from16[2])
+{
+    const std::string path = calib_path(false);
+    FILE *f = path.empty() ? nullptr : fopen(path.c_str(), "r");
+    if (!f)
+        return false;
+    bool found = false;
+    char line[1024], k[800];
+    while (fgets(line, sizeof line, f)) {
+        unsigned x, y;
+        if (sscanf(line, "%799s %u %u", k, &x, &y) == 3 && key == k) {
+            from16[0] = x;
+            from16[1] = y;
+            found = true;
+        }
+    }
+    fclose(f);
+    return found;
+}
+
+void calib_save(const std::string &key, const uint32_t from16[2])
+{
+    const std::string path = calib_path(true);
+    FILE *f = path.empty() ? nullptr : fopen(path.c_str(), "a");
+    if (!f)
+        return;
+    fprintf(f, "%s %u %u\n", key.c_str(), from16[0], from16[1]);
+    fclose(f);
 }
 
 /* milliseconds of the faster of three calls of this way, or -1 */
@@ -491,6 +565,7 @@ void calibrate(janas_attn *a)
     a->calibrated = 1;
     const uint64_t rows0 = a->part_rows;
     a->from16[0] = a->from16[1] = UINT32_MAX;
+    const std::string key = calib_key(a);
     {
         std::lock_guard<std::mutex> lk(g_calib_mu);
         if (g_calib)
@@ -500,6 +575,13 @@ void calibrate(janas_attn *a)
                     a->from16[1] = c.from16[1];
                     return;
                 }
+        if (calib_load(key, a->from16)) {
+            if (!g_calib)
+                g_calib = new std::vector<Calib>();
+            g_calib->push_back(Calib{a->dev, a->ring, a->n_head, a->n_kv, a->hd, a->window,
+                                     a->n_ctx, {a->from16[0], a->from16[1]}});
+            return;
+        }
     }
     const uint32_t nb = JANAS_ATTN_MAX_BLOCK < 64 ? JANAS_ATTN_MAX_BLOCK : 64;
     const uint32_t top = !a->ring && a->n_ctx > 65536 + nb ? 65536 + nb : a->n_ctx;
@@ -591,6 +673,7 @@ void calibrate(janas_attn *a)
         g_calib = new std::vector<Calib>();
     g_calib->push_back(Calib{a->dev, a->ring, a->n_head, a->n_kv, a->hd, a->window, a->n_ctx,
                              {a->from16[0], a->from16[1]}});
+    calib_save(key, a->from16);
 }
 
 /* The engine's choice for a call of n tokens at pos0 (janas_attn_run,

@@ -14,6 +14,20 @@ def pytest_configure(config):
         "markers", "gpu: needs an MI355X (runs the HIP library on cuda:0)")
 
 
+@pytest.fixture(scope="session", autouse=True)
+def _cache_dir(tmp_path_factory):
+    """AUTO's measurements persist in the cache directory
+    ($XDG_CACHE_HOME/janas): the session gets an empty one of its own, so
+    no earlier run's file decides a test's way."""
+    old = os.environ.get("XDG_CACHE_HOME")
+    os.environ["XDG_CACHE_HOME"] = str(tmp_path_factory.mktemp("cache"))
+    yield
+    if old is None:
+        os.environ.pop("XDG_CACHE_HOME", None)
+    else:
+        os.environ["XDG_CACHE_HOME"] = old
+
+
 @pytest.fixture(scope="session")
 def gpu():
     """The GPU tests run where a GPU is: fail, never skip, without one."""

@@ -392,3 +392,46 @@ def test_auto_long_prompt_first_call(gpu, monkeypatch, n_ctx, n):
                   kv=orc.KV_I8, threads=threads(), block=64)
     assert within(abs_err(first, ref), TOL_FLOAT_ABS,
                   f"AUTO first call, {n} tokens")
+
+
+def test_auto_measurement_persists(gpu, monkeypatch, tmp_path):
+    """AUTO's measurement is kept in attn_gpu.txt under the cache directory
+    ($XDG_CACHE_HOME/janas, as the reference keeps attn.txt,
+    attention.c:1118-1164), one line "key from16[0] from16[1]" keyed by
+    device and geometry; a geometry found there is taken without measuring.
+    A line saying INT16 from 2048 (one token) makes a call at 4000 the
+    INT16 way's bits and a call at 1500 the FLOAT way's."""
+    monkeypatch.setenv("XDG_CACHE_HOME", str(tmp_path))
+    monkeypatch.delenv("JANAS_ATTN", raising=False)
+    h, kvh, hd, cap = 8, 2, 128, 4400
+    k, ks = int8_cache(621, kvh, cap, hd)
+    v, vs = int8_cache(622, kvh, cap, hd)
+    q = normal(623, h * hd).reshape(1, h, hd)
+    kd, vd, ksd, vsd, qd = (to_dev(x, gpu) for x in (k, v, ks, vs, q))
+
+    def call(n_ctx, scores, pos0):
+        out = torch.zeros((1, h, hd), dtype=torch.float32, device=gpu)
+        with Attention(h, kvh, hd, n_ctx, 1, scores) as a:
+            a.run_dev(janas_amd.KV_I8, [dict(k=kd, v=vd, ks=ksd, vs=vsd, q=qd,
+                                              out=out, cap=cap, n=1,
+                                              pos0=pos0)])
+            torch.cuda.synchronize()
+            way = a.scores_mode()
+        return way, out.cpu().numpy()
+
+    # a fresh geometry is measured, and its line written
+    call(4321, janas_amd.AUTO, 4000)
+    path = tmp_path / "janas" / "attn_gpu.txt"
+    lines = [l for l in path.read_text().splitlines() if l.strip()]
+    key, f0, f1 = lines[-1].split()
+    assert key.endswith("|0|8/2/128|0|4321"), key
+    assert int(f0) >= 1024 and int(f1) >= 1024
+    # another geometry's line, as if an earlier process had measured INT16
+    key2 = key[:-len("4321")] + "4322"
+    with open(path, "a") as f:
+        f.write(f"{key2} 2048 1024\n")
+    for pos0, want in ((4000, janas_amd.INT16), (1500, janas_amd.FLOAT)):
+        way, got = call(4322, janas_amd.AUTO, pos0)
+        assert way == want
+        _, ref = call(4322, want, pos0)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
