@@ -66,20 +66,36 @@ def test_noalloc_equals_run_dev_twice(gpu):
     assert torch.equal(ob, ob2)
 
 
-def test_noalloc_refuses_more_than_the_array(gpu):
-    """A 64-token block at 32k over 8 KV heads of 128 needs 8 x 128 x 64 x 4
-    partial rows of 130 floats (34 MB) - fits; at 64k it needs twice that."""
-    h, kvh, hd, L = 32, 8, 128, 65536
+@pytest.mark.parametrize("L,fits", [(16128, True), (16384, False), (65536, False)])
+def test_noalloc_refuses_more_than_the_array(gpu, L, fits):
+    """The array's capacity for the split path's partials: a row of m, l and
+    hd values takes (hd + 2) x 4 bytes, a launch n_kv x chunks x n x group
+    rows (the m, l pairs padded to 256 bytes). A 64-token block over 8 KV
+    heads of 128 (32 query heads) at positions L - 64 .. L - 1 takes 2048
+    rows a chunk: 63 chunks (L = 16128: 67,092,480 bytes) fit in the
+    67,108,864, 64 chunks (L = 16384: 68,157,440) do not and are refused
+    with ERANGE, as is 64k. The block that fits equals janas_attn_run_dev's
+    result bit for bit."""
+    h, kvh, hd = 32, 8, 128
     k = torch.zeros((kvh, L, hd), dtype=torch.float16, device=gpu)
-    q = torch.zeros((64, h, hd), dtype=torch.float32, device=gpu)
-    out = torch.empty_like(q)
+    q = dev(normal(161, 64 * h * hd).reshape(64, h, hd), gpu)
+    out = torch.full_like(q, float("nan"))
+    chunks = (L + 255) // 256
+    rows = kvh * chunks * 64 * (h // kvh)
+    need = (rows * 2 * 4 + 255) // 256 * 256 + rows * hd * 4
+    assert (need <= NOALLOC_BYTES) == fits
+    seq = dict(k=k, v=k, q=q, out=out, cap=L, n=64, pos0=L - 64)
     with Attention(h, kvh, hd, L) as a:
-        rows = kvh * (L // 256) * 64 * (h // kvh)
-        assert rows * (hd + 2) * 4 > NOALLOC_BYTES
-        with pytest.raises(janas_amd.AttnError) as e:
-            a.run_dev(janas_amd.KV_F16, [dict(k=k, v=k, q=q, out=out, cap=L,
-                                              n=64, pos0=L - 64)], path="noalloc")
-        assert e.value.code == janas_amd.ERANGE
+        if not fits:
+            with pytest.raises(janas_amd.AttnError) as e:
+                a.run_dev(janas_amd.KV_F16, [seq], path="noalloc")
+            assert e.value.code == janas_amd.ERANGE
+            return
+        a.run_dev(janas_amd.KV_F16, [seq], path="noalloc")
+        want = torch.full_like(q, float("nan"))
+        a.run_dev(janas_amd.KV_F16, [dict(seq, out=want)])
+        torch.cuda.synchronize()
+    assert torch.equal(out, want)
 
 
 def test_noalloc_under_graph_capture(gpu):
