@@ -738,6 +738,19 @@ uint32_t prefill_segments(const janas_attn *a, const SeqDesc &d, bool halves, in
     return (uint32_t)std::min<uint64_t>(want, kMaxSegs);
 }
 
+/* Whether the prefill kernels write the Q8_K blocks with their output
+   (write_out): a block is 256 / hd whole rows of one token's heads, so
+   hd is 64, 128 or 256 - a whole number of rows a block, no padding - and
+   the rows of a block (consecutive heads) are in one KV head's group. The
+   register-staged kernel (hd 512), the exact kernel at 256 and other head
+   sizes leave it to a pass over the output, unless a segment merge writes
+   it. */
+bool prefill_q8k_fused(const janas_attn *a)
+{
+    const uint32_t hd = a->hd;
+    return (hd == 64 || hd == 128 || hd == 256) && a->group % (256 / hd) == 0;
+}
+
 /* Whether a prefill sequence takes the two-halves kernel (128 rows a
    workgroup as two key groups, prefill_half_kernel): f16 rows of 72..128
    numbers whose workgroups in the DMA kernel, key segments included, would
@@ -819,6 +832,7 @@ int run_prefill_launch(janas_attn *a, int kv, int gate_mode,
             args.gate_mode = gate_mode;
             args.halves = hv;
             args.exact = exact;
+            args.q8k_fused = prefill_q8k_fused(a) && !(exact && a->hd > 128);
             ProfEv *ev = fixed ? nullptr : prof_begin(a, 2, stream);
             hipError_t e = launch_prefill(kv, args, stream);
             if (e == hipSuccess && mg)
@@ -826,7 +840,11 @@ int run_prefill_launch(janas_attn *a, int kv, int gate_mode,
             prof_end(ev, stream);
             if (e != hipSuccess)
                 return hip_err(e, "prefill launch");
+            /* Q8_K: the kernel's output or the segment merge wrote the
+               blocks, or else a pass over the output does */
             for (uint32_t j = 0; j < m; j++) {
+                if (args.q8k_fused || args.seq[j].nseg > 1)
+                    continue;
                 int rc = put_q8k(a, picked[j], 1, stream);
                 if (rc)
                     return rc;

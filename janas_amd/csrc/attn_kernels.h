@@ -92,6 +92,10 @@ struct PrefillArgs {
     int gate_mode;
     int halves;            /* the two-halves kernel (prefill_halves_supported):
                               128 rows a workgroup, two key groups */
+    int q8k_fused;         /* the kernel writes a sequence's Q8_K blocks
+                              with its output (head size 64, 128 or 256, a
+                              block's rows in one wave); the segment merge
+                              always does */
     int exact;             /* int8 / int16 at float accuracy
                               (prefill_exact_kernel): the planes of the copy
                               the sequences' k and v point at (1 int8, 2

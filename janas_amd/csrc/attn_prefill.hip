@@ -69,6 +69,7 @@
 #include <hip/hip_runtime.h>
 
 #include "attn_kernels.h"
+#include "attn_q8k.h"
 
 namespace janas {
 namespace {
@@ -515,14 +516,59 @@ __device__ __forceinline__ void tile_pass(uint32_t p0, const PBlock &P, const h8
     }
 }
 
-/* out = sums / weights, gated */
+/* write_out for a sequence that asks for Q8_K when the kernel writes its
+   blocks (A.q8k_fused: head size D exactly, 64, 128 or 256, a block's rows
+   in one wave): the output and its blocks from the same numbers */
 template <int D>
+__device__ __forceinline__ void write_out_q8k(const PrefillArgs &A, const PBlock &P, float lt,
+                                           f16x *x)
+{
+    constexpr int CT = D / 32;
+    const uint32_t g = (threadIdx.x & 63) >> 5, hd = A.hd;
+    const SeqDesc &sq = *P.sq;
+    const float inv = 1.0f / lt;
+    const size_t obase = ((size_t)P.rj * A.n_head + P.rh) * hd;
+    /* the sums become the outputs in place */
+#pragma unroll
+    for (int c = 0; c < CT; c++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t col = 32 * c + 8 * (i / 4) + 4 * g + i % 4;
+            float v = x[c][i] * inv;
+            if (A.gate_mode == kGateElem)
+                v *= 1.0f / (1.0f + expf(-sq.gate[P.rok ? obase + col : 0]));
+            else if (A.gate_mode == kGateHead)
+                v *= 1.0f / (1.0f + expf(-sq.gate[P.rok ? (size_t)P.rj * A.n_head + P.rh : 0]));
+            x[c][i] = P.rok ? v : 0.0f;
+        }
+    if (P.rok)
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++)
+                *(float4 *)(sq.out + obase + 32 * c + 8 * q4 + 4 * g) =
+                    float4{x[c][4 * q4], x[c][4 * q4 + 1], x[c][4 * q4 + 2], x[c][4 * q4 + 3]};
+    uint8_t *dst = (uint8_t *)sq.q8k +
+                   ((size_t)P.rj * (A.n_head * D / 256) + P.rh / (256 / D)) * kQ8kBytes;
+    q8k_rows<CT>(x, dst, P.rok);
+}
+
+/* out = sums / weights, gated (and its Q8_K blocks: write_out_q8k, which
+   turns o into the outputs in place; QF false: not compiled in, the
+   host leaves those blocks to a pass) */
+template <int D, bool QF = true>
 __device__ __forceinline__ void write_out(const PrefillArgs &A, const PBlock &P,
-                                          float lsum, const f16x *o)
+                                          float lsum, f16x *o)
 {
     const uint32_t g = (threadIdx.x & 63) >> 5, hd = A.hd;
     const SeqDesc &sq = *P.sq;
     const float lt = lsum + __shfl_xor(lsum, 32, 64);
+    if constexpr (QF && (D == 64 || D == 128 || D == 256)) {
+        if (A.q8k_fused && sq.q8k) {
+            write_out_q8k<D>(A, P, lt, o);
+            return;
+        }
+    }
     if (!P.rok)
         return;
     const float inv = 1.0f / lt;
@@ -551,12 +597,12 @@ __device__ __forceinline__ void write_out(const PrefillArgs &A, const PBlock &P,
    segment's partial - largest score m (log2 units, -inf when the row saw
    nothing of it), sum of weights, unnormalised weighted values - for the
    ordered merge (pmerge_kernel); otherwise the output itself */
-template <int D>
+template <int D, bool QF = true>
 __device__ __forceinline__ void finish(const PrefillArgs &A, const PBlock &P,
-                                       float m, float lsum, const f16x *o)
+                                       float m, float lsum, f16x *o)
 {
     if (P.nseg == 1) {
-        write_out<D>(A, P, lsum, o);
+        write_out<D, QF>(A, P, lsum, o);
         return;
     }
     const uint32_t g = (threadIdx.x & 63) >> 5, hd = A.hd;
@@ -736,6 +782,19 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_kernel(const PrefillA
  *
  * Two buffer pairs, as distinct arrays, and the tile loop unrolled by two.
  */
+/* a value the same in every lane, said so (the compiler cannot always
+   prove it, and a scalar operand needs it); the builtin returns int, so
+   each half is widened unsigned */
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t b)
+{
+    return (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b) |
+           (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32;
+}
+template <class T> __device__ __forceinline__ T *uniform_ptr(T *p)
+{
+    return (T *)(uintptr_t)uniform_u64((uint64_t)(uintptr_t)p);
+}
+
 /*
  * One 16-byte-a-lane load from global memory straight into LDS
  * (global_load_lds_dwordx4: lane l's 16 bytes at gbase + voff land at LDS
@@ -755,7 +814,8 @@ __device__ __forceinline__ void dma16(const char *gbase, uint32_t voff, char *ld
 {
     const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds;
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                 :: "s"(__builtin_amdgcn_readfirstlane(m0)), "v"(voff), "s"(gbase));
+                 :: "s"(__builtin_amdgcn_readfirstlane(m0)), "v"(voff),
+                    "s"(uniform_ptr(gbase)));
 }
 
 template <int D> __device__ __forceinline__ uint32_t swz(uint32_t r)
@@ -811,8 +871,10 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
     /* held in registers: read through P.sq inside the loop they would be
        reloaded after every load into LDS, and a pending scalar load makes
        each LDS operand wait drain the whole queue */
-    const char *const kg = (const char *)sq.k, *const vg = (const char *)sq.v;
-    const uint32_t cap = sq.cap, rbytes = hd * 2;
+    const char *const kg = uniform_ptr((const char *)sq.k);
+    const char *const vg = uniform_ptr((const char *)sq.v);
+    const uint32_t cap = __builtin_amdgcn_readfirstlane(sq.cap), rbytes = hd * 2;
+    const size_t head_row = uniform_u64(P.head_row);
     const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
     /* a tile's rows are contiguous in the cache (a ring's capacity is a
        multiple of 256 positions): one base a tile, in scalar registers, and
@@ -820,7 +882,7 @@ __global__ __launch_bounds__(PCfg<D>::W * 64) void prefill_dma_kernel(const Pref
        nearest one inside [lo_all, hi_all], which lies in the same tile */
     auto tbase = [&](uint32_t tile) -> size_t {
         const uint32_t t0 = tile * kTile;
-        return (P.head_row + (ring ? t0 % cap : t0)) * rbytes;
+        return (head_row + (ring ? t0 % cap : t0)) * rbytes;
     };
     /* the lane's byte offsets in tile `tile` for its NJ load rows */
     auto offsets = [&](uint32_t tile, uint32_t *off) {
@@ -1243,7 +1305,8 @@ __global__ __launch_bounds__((PCfg<D, false, (T == kI16 ? 2 : 1)>::W) * 64) void
     const uint32_t pb = sq.c0 * kChunk, np = sq.end - pb;
     const uint32_t rbytes = hd * 2;
     const size_t pstride = (size_t)A.n_kv * np * rbytes;
-    const char *const kg = (const char *)sq.k, *const vg = (const char *)sq.v;
+    const char *const kg = uniform_ptr((const char *)sq.k);
+    const char *const vg = uniform_ptr((const char *)sq.v);
     const uint32_t wu = __builtin_amdgcn_readfirstlane(w);
     const uint32_t drow = RPI * w + lane / UPR;
     uint32_t dcol[NJ];
@@ -1357,7 +1420,9 @@ __global__ __launch_bounds__((PCfg<D, false, (T == kI16 ? 2 : 1)>::W) * 64) void
         if (tile + 2 > P.tlast)
             break;
     }
-    finish<D>(A, P, m, lsum, o);
+    /* head size 256: the Q8_K epilogue's registers would spill into the
+       tile loop of this one-wave-a-SIMD kernel; a pass does it */
+    finish<D, (D < 256)>(A, P, m, lsum, o);
 }
 
 /*
@@ -1487,11 +1552,13 @@ __global__ __launch_bounds__((PCfg<D, true>::W) * 64) void prefill_half_kernel(c
         const uint32_t unit = (lane % UPR) ^ swz<D>(drow + RPI * kGW * j);
         dcol[j] = unit * 8 < hd ? unit * 8 : 0;
     }
-    const char *const kg = (const char *)sq.k, *const vg = (const char *)sq.v;
-    const uint32_t cap = sq.cap, rbytes = hd * 2;
+    const char *const kg = uniform_ptr((const char *)sq.k);
+    const char *const vg = uniform_ptr((const char *)sq.v);
+    const uint32_t cap = __builtin_amdgcn_readfirstlane(sq.cap), rbytes = hd * 2;
+    const size_t head_row = uniform_u64(P.head_row);
     auto fetch = [&](uint32_t tile, char *dk, char *dv) __attribute__((always_inline)) {
         const uint32_t t0 = tile * kTile;
-        const size_t base = (P.head_row + (ring ? t0 % cap : t0)) * rbytes;
+        const size_t base = (head_row + (ring ? t0 % cap : t0)) * rbytes;
 #pragma unroll
         for (int j = 0; j < (int)NJ; j++) {
             uint32_t p = t0 + drow + RPI * kGW * j;
@@ -1612,6 +1679,8 @@ __global__ __launch_bounds__(kPMergeThreads) void pmerge_kernel(const PrefillArg
     const uint32_t hd = A.hd, nseg = sq.nseg, c4 = hd / 4;
     const uint64_t pair = (uint64_t)(id - sq.mg0) * kPMergeThreads + threadIdx.x;
     const uint32_t row = (uint32_t)(pair / c4), col = (uint32_t)(pair % c4) * 4;
+    /* past the sequence's rows: whole waves, since with Q8_K its outputs
+       are whole blocks of 64 pairs */
     if (row >= sq.n * A.n_head)
         return;
     const uint32_t j = row / A.n_head, h = row % A.n_head;
@@ -1666,6 +1735,12 @@ __global__ __launch_bounds__(kPMergeThreads) void pmerge_kernel(const PrefillArg
             x[e] *= 1.0f / (1.0f + expf(-sq.gate[(size_t)j * A.n_head + h]));
     }
     *(float4 *)(sq.out + oi) = float4{x[0], x[1], x[2], x[3]};
+    /* the output's Q8_K blocks: a thread's 4 numbers are 4 of a block, a
+       wave's 64 threads one whole block (the pairs run through the output
+       in order, 4 numbers a pair, and every wave's first pair is a multiple
+       of 64) */
+    if (sq.q8k)
+        q8k_wave4(x, (uint8_t *)sq.q8k + (pair / 64) * kQ8kBytes, true);
 }
 
 template <int T, int D>

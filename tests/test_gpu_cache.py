@@ -336,3 +336,64 @@ def test_written_cache_attends_like_the_reference(gpu, kv):
     ref = orc.run(q, kc, vc, kz, vz, n_head=h, n_kv=kvh, hd=hd,
                   pos0=npos - 4, kv=kv, threads=threads())
     assert within(abs_err(out.cpu().numpy(), ref), TOL_FLOAT_ABS, "abs_err(out.cpu().numpy(), ref)")
+
+
+@pytest.mark.parametrize("geom", [
+    (32, 8, 128, 2048, 0, KV_F16),     # DMA kernel, one segment: write_out
+    (32, 8, 128, 1024, 0, KV_F16),     # two-halves kernel
+    (32, 8, 128, 300, 600, KV_F16),    # key segments: the segment merge
+    (16, 2, 256, 700, 100, KV_F16),    # a block is one row
+    (16, 4, 64, 900, 0, KV_F16),       # a block is four rows
+    (32, 8, 128, 800, 0, KV_I8),       # the exact kernel
+    (16, 2, 256, 600, 0, KV_I16),      # the exact kernel, two planes
+    (8, 2, 96, 300, 0, KV_F16),        # no whole rows a block: a pass
+    (8, 8, 128, 400, 0, KV_F16),       # a block's heads in two KV heads
+    (4, 1, 512, 200, 0, KV_F16),       # the register-staged kernel
+])
+@pytest.mark.parametrize("gate_mode", [jm.GATE_NONE, jm.GATE_ELEM])
+def test_prefill_q8k(gpu, geom, gate_mode):
+    """A prompt that asks for Q8_K output on the prefill path: the kernel
+    writes the blocks with its output (head sizes 64, 128, 256, a block's
+    heads in one KV head's group), the segment merge with its, or a pass
+    over the output does (other shapes). Every way: the blocks equal the
+    restatement of janas_q8k_quantize over the output bit for bit, and the
+    output equals the same sequence's without Q8_K bit for bit, both in one
+    launch and alone."""
+    h, kvh, hd, n, pos0, kv = geom
+    L = pos0 + n
+    rng = np.random.default_rng(hd + n + kv)
+    if kv == KV_F16:
+        k = rng.standard_normal((kvh, L, hd)).astype(np.float16)
+        v = rng.standard_normal((kvh, L, hd)).astype(np.float16)
+        ks = vs = None
+    else:
+        top = 127 if kv == KV_I8 else 32767
+        dt = np.int8 if kv == KV_I8 else np.int16
+        kf = rng.standard_normal((kvh, L, hd)).astype(np.float32)
+        vf = rng.standard_normal((kvh, L, hd)).astype(np.float32)
+        ks = (np.abs(kf).max(axis=2) / top).astype(np.float32)
+        vs = (np.abs(vf).max(axis=2) / top).astype(np.float32)
+        k = np.rint(kf / ks[..., None]).astype(dt)
+        v = np.rint(vf / vs[..., None]).astype(dt)
+    q = rng.standard_normal((n, h, hd)).astype(np.float32)
+    g = rng.standard_normal((n, h, hd)).astype(np.float32)
+    seq = dict(k=dev(k, gpu), v=dev(v, gpu), q=dev(q, gpu), gate=dev(g, gpu),
+               cap=L, n=n, pos0=pos0)
+    if ks is not None:
+        seq.update(ks=dev(ks, gpu), vs=dev(vs, gpu))
+    outs = [torch.full((n, h, hd), float("nan"), device=gpu) for _ in range(3)]
+    blocks = torch.zeros((n, h * hd // 256, jm.attention.Q8K_BYTES),
+                         dtype=torch.uint8, device=gpu)
+    with jm.Attention(h, kvh, hd, L, 1, jm.FLOAT) as a:
+        a.run_dev(kv, [dict(seq, out=outs[0], out_q8k=blocks),
+                       dict(seq, out=outs[1])], gate_mode=gate_mode,
+                  path="prefill")
+        a.run_dev(kv, [dict(seq, out=outs[2])], gate_mode=gate_mode,
+                  path="prefill")
+        torch.cuda.synchronize()
+        assert a.status() == 0
+    o = [x.cpu().numpy() for x in outs]
+    assert np.array_equal(o[0].view(np.int32), o[2].view(np.int32))
+    assert np.array_equal(o[1].view(np.int32), o[2].view(np.int32))
+    want = orc.q8k_quantize(o[0].reshape(n, h * hd))
+    assert blocks.cpu().numpy().tobytes() == want.tobytes()
