@@ -564,6 +564,9 @@ def main():
                                        "gemm", "configs", "int"),
                     help="run one leg alone (profiling)")
     ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--kv", choices=("f16", "int8", "int16"), default="f16",
+                    help="--only prefill: the cache's element type (int8 / "
+                         "int16: the prompt's rows quantized, per-row scales)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is "
@@ -590,8 +593,15 @@ def main():
         return
     if args.only == "prefill":
         wp = prefill_workload()
-        pms = bench_prefill(torch, jm, wp, args.prefill_steps, 3)
-        print(json.dumps({"prefill_ms": pms}), flush=True)
+        kv = None
+        if args.kv != "f16":
+            dt = np.int8 if args.kv == "int8" else np.int16
+            k, ks = quantized(wp["k"], dt)
+            v, vs = quantized(wp["v"], dt)
+            wp = dict(wp, k=k, v=v, ks=ks, vs=vs)
+            kv = jm.KV_I8 if args.kv == "int8" else jm.KV_I16
+        pms = bench_prefill(torch, jm, wp, args.prefill_steps, 3, kv=kv)
+        print(json.dumps({"prefill_ms": pms, "kv": args.kv}), flush=True)
         return
     if args.only == "wide":
         print(json.dumps(wide_leg(torch, jm, args.steps, args.warmup)),
