@@ -6,7 +6,9 @@ ones). The cases are the same on every run; each prints its draw first.
 
 Bars: the split path is float-accurate (f32 cache: max |err| / max |ref|
 1e-5; int8 / int16 / f16: 1e-5 of max(1, max |ref|), the reference's FLOAT
-bar, test_attention.c:146); the prefill path computes in f16 (2e-3 abs).
+bar, test_attention.c:146); so is the prefill path over int8 / int16 caches
+up to head size 256 (the exact kernel); over f16 caches, and at head size
+512, it computes in f16 (2e-3 abs).
 """
 import numpy as np
 import pytest
@@ -114,7 +116,8 @@ def test_random_geometry(gpu, i):
     if gate is not None:
         orc.gate(ref, gate, per_head=g["gate"] == 2)
     assert np.isfinite(out).all()
-    if g["path"] == "prefill":
+    exact = g["kv"] in (KV_I8, KV_I16) and hd <= 256
+    if g["path"] == "prefill" and not exact:
         err, bar = abs_err(out, ref), TOL_F16_ABS
     elif g["kv"] == KV_F32:
         err, bar = rel_err(out, ref), TOL_F32_REL
@@ -163,3 +166,72 @@ def test_random_many_sequences(gpu, path):
     bar = TOL_F16_ABS if path == "prefill" else TOL_FLOAT_ABS
     print(f"{path}: worst err {worst:.2e} (bar {bar:.0e})")
     assert within(worst, bar, "worst vs oracle")
+
+
+def draw_exact(i):
+    """Case i of the exact kernel's geometries: int8 or int16, head sizes up
+    to 256 (padded ones too), any group, windows, rings, gates, prompts of
+    65 to 700 tokens."""
+    z = [int(x) for x in splitmix(7500 + i, 12)]
+    kv = [KV_I8, KV_I16][z[0] % 2]
+    hd = [40, 64, 96, 128, 200, 256][z[1] % 6]
+    group = [1, 2, 3, 4, 8][z[2] % 5]
+    n_kv = 1 + z[3] % 3
+    n = 65 + z[4] % 636
+    pos0 = z[5] % 2000
+    window = 0 if z[6] % 2 else 64 + z[7] % 1200
+    ring = window > 0 and z[8] % 3 == 0
+    gate = z[9] % 3
+    cap = CHUNK * ((window + n) // CHUNK + 3) if ring else pos0 + n + z[10] % 200
+    return dict(kv=kv, hd=hd, n_head=group * n_kv, n_kv=n_kv, n=n, pos0=pos0,
+                window=window, ring=ring, gate=gate, cap=cap, path="prefill",
+                seed=9600 + 10 * i)
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_random_exact_prefill(gpu, i):
+    """The exact kernel on seeded random geometries, two sequences a launch
+    (the second a shorter, later call over the same cache, so their copies
+    sit at different offsets), each within the FLOAT bar of the
+    restatement."""
+    g = draw_exact(i)
+    print(f"case {i}: {g}", flush=True)
+    k, v, ks, vs, q, gate = inputs(g)
+    n, h, hd = g["n"], g["n_head"], g["hd"]
+    n2 = max(1, n // 3)
+    p2 = g["pos0"] + n - n2
+    calls = [(q, g["pos0"], n, gate), (q[-n2:], p2, n2,
+                                       None if gate is None else gate[-n2:])]
+    gate_mode = 0 if gate is None else (janas_amd.GATE_ELEM if g["gate"] == 1
+                                        else janas_amd.GATE_HEAD)
+    dev = []
+    for qq, p, m, gg in calls:
+        d = dict(k=to_dev(k, gpu), v=to_dev(v, gpu), ks=to_dev(ks, gpu),
+                 vs=to_dev(vs, gpu), q=to_dev(qq, gpu),
+                 out=torch.full((m, h, hd), float("nan"), device=gpu),
+                 cap=g["cap"], n=m, pos0=p)
+        if gg is not None:
+            d["gate"] = to_dev(gg, gpu)
+        dev.append(d)
+    with Attention(h, g["n_kv"], hd, g["cap"]) as a:
+        if g["window"]:
+            a.set_window(g["window"])
+        if g["ring"]:
+            a.set_ring(True)
+        a.prof_enable(True)
+        a.run_dev(g["kv"], dev, gate_mode=gate_mode, path="prefill")
+        torch.cuda.synchronize()
+        assert a.prof_read()["split"][0] == 0
+    worst = 0.0
+    for (qq, p, m, gg), d in zip(calls, dev):
+        ref = orc.run(np.ascontiguousarray(qq, np.float32), k, v, ks, vs,
+                      n_head=h, n_kv=g["n_kv"], hd=hd, pos0=p, kv=g["kv"],
+                      window=g["window"], ring=g["ring"], threads=threads(),
+                      block=64)
+        if gg is not None:
+            orc.gate(ref, gg, per_head=g["gate"] == 2)
+        out = d["out"].cpu().numpy()
+        assert np.isfinite(out).all()
+        worst = max(worst, abs_err(out, ref) / max(1.0, float(np.abs(ref).max())))
+    print(f"case {i}: worst err {worst:.2e}")
+    assert within(worst, TOL_FLOAT_ABS, "exact prefill vs oracle")
