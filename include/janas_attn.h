@@ -57,9 +57,14 @@ extern "C" {
    reference's janas_attn_run does (attention.c:1183-1262), AUTO over an
    int8 cache measures both ways once, on the device, at its first call,
    and each call takes INT16 from the position measured on (per one token
-   and per block): janas_attn_scores_mode reports the last call's way. A
-   Part 2 call of one sequence on the split path chooses the same way; one
-   captured into a graph before any measurement keeps the last one. */
+   and per block): janas_attn_scores_mode reports the last call's way. The
+   measurement is kept in attn_gpu.txt under the cache directory
+   ($XDG_CACHE_HOME/janas, else ~/.cache/janas) by device and geometry, as
+   the reference keeps attn.txt there, and a later process takes it from
+   there. A Part 2 call of any length and any number of sequences measures
+   at its first call outside graph capture (the allocation-free entry point
+   never does) and chooses the same way - a call of several sequences INT16
+   only when each would; until measured, AUTO computes FLOAT. */
 enum janas_attn_scores {
     JANAS_ATTN_AUTO = 0,
     JANAS_ATTN_FLOAT = 1,
@@ -184,9 +189,15 @@ struct janas_attn_q8k {
  * ring and scores way (INT16 for int8 caches) apply to all. Blocks of up to
  * JANAS_ATTN_MAX_BLOCK tokens a sequence take the split-KV path, whose
  * chunking matches janas_attn_run bit for bit token by token; longer
- * prompts take the MFMA prefill path (causal tiles, f16 query and weights:
- * equal within 2e-3 of softmax-normalized outputs) - except int8 caches
- * under INT16, which stay on the split-KV path at any length. A prompt whose row blocks alone would
+ * prompts take the MFMA prefill path - except int8 caches under INT16, which
+ * stay on the split-KV path at any length. Over f16 caches the prefill path
+ * computes with an f16 query and weights (within 2e-3 of softmax-normalized
+ * outputs); over int8 and int16 caches up to head_dim 256 it is
+ * float-accurate like the reference's FLOAT way (the cached integers exact,
+ * the query and the weights as two f16 planes each, within 1e-5), over a
+ * copy of the rows the call sees that the instance holds (2 x planes x
+ * n_head_kv x positions x head_dim x 2 bytes; planes 1 for int8, 2 for
+ * int16). A prompt whose row blocks alone would
  * leave compute units idle (a short prompt, a chunk of a long one) has its
  * key range split into segments, merged in order through the partials; the
  * split depends on the sequence and the device alone, so its result is the
@@ -205,10 +216,12 @@ int janas_attn_run_dev_split(struct janas_attn *a, int kv_type, int gate_mode,
                              uint32_t n_seqs, void *stream);
 
 /* The same, always through the MFMA prefill path: f16, int8 and int16
-   caches (the latter two dequantized into f16 as tiles are staged),
-   head_dim up to 512 (JANAS_ATTN_ENOTSUP for f32 caches;
+   caches, head_dim up to 512 (JANAS_ATTN_ENOTSUP for f32 caches;
    janas_attn_run_dev then takes the split-KV path). Its arithmetic is the
-   f16 one whatever the instance's scores way. */
+   FLOAT way's whatever the instance's scores way: float-accurate over int8
+   and int16 caches up to head_dim 256, f16 query and weights over f16
+   caches, and rows dequantized into f16 over int8 / int16 caches at
+   head_dim 264..512. */
 int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
                                int gate_mode,
                                const struct janas_attn_seq *seqs,
@@ -217,10 +230,11 @@ int janas_attn_run_dev_prefill(struct janas_attn *a, int kv_type,
 /*
  * janas_attn_run_dev without any allocation, for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops that
- * forbid it). No counterpart in the reference. The partials live in one
- * fixed array of JANAS_ATTN_NOALLOC_BYTES that each GPU holds from the
- * library's first janas_attn_create on it until the process ends, instead
- * of the instance's; a call that needs more returns JANAS_ATTN_ERANGE. Calls
+ * forbid it). No counterpart in the reference. The partials, and the copy
+ * of an int8 / int16 prompt's rows, live in one fixed array of
+ * JANAS_ATTN_NOALLOC_BYTES that each GPU holds from the library's first
+ * janas_attn_create on it until the process ends, instead of the
+ * instance's; a call that needs more returns JANAS_ATTN_ERANGE. Calls
  * that overlap on one GPU (any instance, any stream) share that array and
  * race: the caller keeps them in order (one stream, or events).
  */
