@@ -48,9 +48,14 @@ __device__ __forceinline__ h4 lds_read_tr(const _Float16 *p)
     return __builtin_bit_cast(h4, v);
 }
 
-/* x = hi + lo, both f16; x already scaled into f16's normal range */
+/* x = hi + lo, both f16; x already scaled into f16's normal range. x is
+   pinned as the f32 number it is: left free, the compiler may form hi from
+   the product that made x, rounded once to f16 (v_fma_mixlo_f16), in one
+   kernel instance and from x in another - different bits for one row in
+   two instances, and hi + lo no longer x. */
 __device__ __forceinline__ void split_hl(float x, _Float16 &hi, _Float16 &lo)
 {
+    asm volatile("" : "+v"(x));
     hi = (_Float16)x;
     lo = (_Float16)(x - (float)hi);
 }
