@@ -481,6 +481,56 @@ def configs_leg(torch, jm, steps=200, warmup=20):
         "ms": round(ms, 5), "value": round(fl / (ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s", "flops": fl, "bound": "mfma",
         "frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+    res.update(host_leg(torch, jm))
+    return res
+
+
+def host_leg(torch, jm, steps=40, warmup=5):
+    """janas_attn_run with everything in host memory, as an engine linked
+    unchanged calls it: the cache staged through the device at every call,
+    and the same calls after janas_attn_import of the cache (only the rows
+    of the call's positions cross PCIe). Host clock around each synchronous
+    call; q and out cross PCIe either way."""
+    res = {}
+
+    def timed(a, args):
+        for _ in range(warmup):
+            a.run(*args)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            a.run(*args)
+        return (time.perf_counter() - t0) * 1e3 / steps
+
+    cases = (
+        ("block64", 32, 8, 128, 4160, 64, 4096),
+        ("decode4", 16, 2, 256, 32768, 1, 32767),
+    )
+    for name, h, kvh, hd, L, n, p0 in cases:
+        rng = np.random.default_rng(SEED + 29)
+        k8, ks8 = quantized(normal(rng, (kvh, L, hd), np.float32), np.int8)
+        v8, vs8 = quantized(normal(rng, (kvh, L, hd), np.float32), np.int8)
+        q = normal(rng, (n, h, hd), np.float32)
+        out = np.zeros_like(q)
+        args = (q, k8, ks8, v8, vs8, n, p0, out)
+        a = jm.Attention(h, kvh, hd, L, 1, jm.FLOAT)
+        if hd == 256:
+            a.set_scale(1.0 / 16.0)
+        staged_ms = timed(a, args)
+        for x in (k8, ks8, v8, vs8):
+            assert a.import_host(x) == 0
+        imported_ms = timed(a, args)
+        a.close()
+        fl = prefill_flops(hd, h, p0, n)
+        kv_bytes = 2 * kvh * L * (hd + 4)
+        res[f"dropin-host-{name}-int8"] = {
+            "workload": f"janas_attn_run, host pointers, {n} token(s) at "
+                        f"positions {p0}..{p0 + n - 1}, {h} / {kvh} heads, "
+                        f"head_dim {hd}, int8 K/V with per-row scales, FLOAT "
+                        "scores; host clock; staged: the cache copied to the "
+                        "device at every call; imported: janas_attn_import "
+                        "once, the call's rows copied",
+            "staged_ms": round(staged_ms, 4), "imported_ms": round(imported_ms, 4),
+            "unit": "ms", "kv_bytes": kv_bytes, "flops": fl}
     return res
 
 

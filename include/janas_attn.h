@@ -125,6 +125,30 @@ void janas_attn_clear_status(struct janas_attn *a);
    returns, the output (host memory) filled with NaN. */
 void janas_attn_set_abort(struct janas_attn *a, int on);
 
+/* A host cache's device copy, the reference's registry of host memory on
+   its GPU (janas_cuda_import / janas_cuda_sync, gpu_cuda.c:372-427; the
+   engine imports each sequence's cache and scales, model_gpu.c:663-666,
+   and syncs them, :527-545). No counterpart in attention.h.
+   janas_attn_import copies host bytes [p, p + bytes) to device memory the
+   instance keeps until janas_attn_forget or destroy. A janas_attn_run whose
+   k, v, ks or vs (the layer's whole n_head_kv x n_ctx rows) lies in an
+   imported range reads its device copy instead of staging the cache over
+   PCIe, after taking from the host the rows of the call's positions, pos0
+   up to the last position a token sees: the rows the engine has just
+   written (model_attn.c writes a block's rows before its attention). Any
+   other change to imported rows on the host - a context shift, a restored
+   state - must be copied over with janas_attn_sync(a, p, bytes, 1) before
+   the next call; janas_attn_sync(a, p, bytes, 0) copies the device's rows
+   back. Both are synchronous. They return 0 or a negative JANAS_ATTN_E*
+   code: EINVAL for a null pointer or 0 bytes, a range overlapping another
+   import only in part, or a sync outside every import; ENOMEM. A range
+   inside one already imported returns 0 and copies nothing.
+   janas_attn_forget drops the import holding p (no-op if none). */
+int janas_attn_import(struct janas_attn *a, const void *p, size_t bytes);
+int janas_attn_sync(struct janas_attn *a, const void *p, size_t bytes,
+                    int to_device);
+void janas_attn_forget(struct janas_attn *a, const void *p);
+
 /* ===== Part 2: the device extension (no counterpart in the reference) = */
 
 enum janas_attn_kv {

@@ -106,6 +106,12 @@ def lib():
     L.janas_attn_clear_status.restype = None
     L.janas_attn_set_abort.argtypes = [_vp, ctypes.c_int]
     L.janas_attn_set_abort.restype = None
+    L.janas_attn_import.argtypes = [_vp, _vp, ctypes.c_size_t]
+    L.janas_attn_import.restype = ctypes.c_int
+    L.janas_attn_sync.argtypes = [_vp, _vp, ctypes.c_size_t, ctypes.c_int]
+    L.janas_attn_sync.restype = ctypes.c_int
+    L.janas_attn_forget.argtypes = [_vp, _vp]
+    L.janas_attn_forget.restype = None
     L.janas_attn_strerror.argtypes = [ctypes.c_int]
     L.janas_attn_strerror.restype = ctypes.c_char_p
     L.janas_attn_cache_write.argtypes = [ctypes.POINTER(Cache), _vp, _vp,
@@ -233,6 +239,21 @@ class Attention:
         """janas_attn_set_abort: whether janas_attn_run aborts on a
         failure (the default) or returns with a NaN output."""
         lib().janas_attn_set_abort(self._a, 1 if on else 0)
+
+    def import_host(self, arr):
+        """janas_attn_import of a host numpy array's bytes (the array
+        must stay alive while imported): 0 or a JANAS_ATTN_E* code."""
+        return lib().janas_attn_import(self._a, ptr(arr), arr.nbytes)
+
+    def sync(self, arr, to_device=True):
+        """janas_attn_sync of a host array (or a view into an imported
+        one)."""
+        return lib().janas_attn_sync(self._a, ptr(arr), arr.nbytes,
+                                     1 if to_device else 0)
+
+    def forget(self, arr):
+        """janas_attn_forget of the import holding arr's first byte."""
+        lib().janas_attn_forget(self._a, ptr(arr))
 
     def prepare(self, kv_type, seqs, gate_mode=GATE_NONE, stream=None,
                 path="auto"):

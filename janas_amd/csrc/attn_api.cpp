@@ -32,6 +32,13 @@ struct ProfEv {
     hipEvent_t a, b;
 };
 
+/* host bytes [host, host + bytes) and their device copy (janas_attn_import) */
+struct HostCopy {
+    const char *host;
+    size_t bytes;
+    char *dev;
+};
+
 }  // namespace
 
 struct janas_attn {
@@ -76,6 +83,8 @@ struct janas_attn {
     /* timing */
     int prof;
     std::vector<ProfEv> *ev_used, *ev_free;
+    /* imported host ranges (janas_attn_import) */
+    std::vector<HostCopy> *copies;
 };
 
 namespace {
@@ -99,6 +108,40 @@ bool is_device_ptr(const void *p)
         return false;
     }
     return at.type == hipMemoryTypeDevice || at.type == hipMemoryTypeManaged;
+}
+
+/* the imported range holding host bytes [p, p + bytes), or null */
+const HostCopy *find_copy(const janas_attn *a, const void *p, size_t bytes)
+{
+    const char *q = (const char *)p;
+    for (const HostCopy &c : *a->copies)
+        if (q >= c.host && bytes <= c.bytes && (size_t)(q - c.host) <= c.bytes - bytes)
+            return &c;
+    return nullptr;
+}
+
+/* A call over an imported cache: the rows of positions [pos0, end) (p mod
+   cap in a ring), each KV head, from the host to the device copy - the rows
+   the call's tokens were just written to. esz: bytes a row. */
+int refresh_rows(janas_attn *a, char *dev, const void *host, size_t esz,
+                 uint32_t pos0, uint32_t end)
+{
+    const size_t cap = a->n_ctx, pitch = cap * esz;
+    size_t lo = a->ring ? pos0 % cap : pos0, n = end - pos0;
+    if (n > cap)
+        n = cap;
+    while (n) {
+        const size_t run = std::min(n, cap - lo);
+        int rc = hip_err(hipMemcpy2DAsync(dev + lo * esz, pitch, (const char *)host + lo * esz,
+                                          pitch, run * esz, a->n_kv, hipMemcpyHostToDevice,
+                                          a->stream),
+                         "copy the call's rows");
+        if (rc)
+            return rc;
+        n -= run;
+        lo = 0;
+    }
+    return JANAS_ATTN_OK;
 }
 
 uint32_t elem_bytes(int kv)
@@ -1052,6 +1095,7 @@ extern "C" struct janas_attn *janas_attn_create(uint32_t n_head,
         a->scores = scores;
     else
         a->scores = n_ctx > 16384 ? JANAS_ATTN_INT16 : JANAS_ATTN_FLOAT;
+    a->copies = new std::vector<HostCopy>();
     a->ev_used = new std::vector<ProfEv>();
     a->ev_free = new std::vector<ProfEv>();
     a->abort_on_error = 1;
@@ -1101,6 +1145,11 @@ extern "C" void janas_attn_destroy(struct janas_attn *a)
     (void)hipFree(a->st_ks);
     (void)hipFree(a->st_vs);
     (void)hipFree(a->st_last);
+    if (a->copies) {
+        for (HostCopy &c : *a->copies)
+            (void)hipFree(c.dev);
+        delete a->copies;
+    }
     for (std::vector<ProfEv> *v : {a->ev_used, a->ev_free})
         if (v) {
             for (ProfEv &ev : *v) {
@@ -1295,6 +1344,18 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
             *x.dst = x.p;
             continue;
         }
+        if (const HostCopy *c = find_copy(a, x.p, x.bytes)) {
+            /* an imported cache: its device copy, with the rows of this
+               call's positions taken from the host first */
+            char *dev = c->dev + ((const char *)x.p - c->host);
+            rc = refresh_rows(a, dev, x.p, x.esz, pos0, end);
+            if (rc) {
+                run_failed(a, "the imported cache", rc, out, qbytes, out_host);
+                return;
+            }
+            *x.dst = dev;
+            continue;
+        }
         if (!staging(x.st, x.have, x.bytes)) {
             run_failed(a, "staging the cache", JANAS_ATTN_ENOMEM, out, qbytes, out_host);
             return;
@@ -1364,6 +1425,81 @@ extern "C" void janas_attn_set_abort(struct janas_attn *a, int on)
 {
     if (a)
         a->abort_on_error = on != 0;
+}
+
+/* The host cache's device copy: janas_cuda_import / janas_cuda_sync
+   (gpu_cuda.c:372-427) - a range is copied to device memory once and found
+   again by its host address. A range inside one already imported is
+   already there; one that overlaps another is refused. */
+extern "C" int janas_attn_import(struct janas_attn *a, const void *p, size_t bytes)
+{
+    if (!a || !p || bytes == 0)
+        return JANAS_ATTN_EINVAL;
+    if (find_copy(a, p, bytes))
+        return JANAS_ATTN_OK;
+    const char *q = (const char *)p;
+    for (const HostCopy &c : *a->copies)
+        if (q < c.host + c.bytes && c.host < q + bytes)
+            return JANAS_ATTN_EINVAL;
+    if (hipSetDevice(a->dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return JANAS_ATTN_EDEVICE;
+    }
+    char *dev = nullptr;
+    if (hipMalloc((void **)&dev, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return JANAS_ATTN_ENOMEM;
+    }
+    int rc = hip_err(hipMemcpyAsync(dev, p, bytes, hipMemcpyHostToDevice, a->stream),
+                     "import");
+    if (!rc)
+        rc = hip_err(hipStreamSynchronize(a->stream), "import");
+    if (rc) {
+        (void)hipFree(dev);
+        return rc;
+    }
+    a->copies->push_back(HostCopy{q, bytes, dev});
+    return JANAS_ATTN_OK;
+}
+
+extern "C" int janas_attn_sync(struct janas_attn *a, const void *p, size_t bytes,
+                               int to_device)
+{
+    if (!a || !p || bytes == 0)
+        return JANAS_ATTN_EINVAL;
+    const HostCopy *c = find_copy(a, p, bytes);
+    if (!c)
+        return JANAS_ATTN_EINVAL;
+    if (hipSetDevice(a->dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return JANAS_ATTN_EDEVICE;
+    }
+    char *dev = c->dev + ((const char *)p - c->host);
+    int rc = to_device ? hip_err(hipMemcpyAsync(dev, p, bytes, hipMemcpyHostToDevice, a->stream),
+                                 "sync to the device")
+                       : hip_err(hipMemcpyAsync((void *)p, dev, bytes, hipMemcpyDeviceToHost,
+                                                a->stream),
+                                 "sync to the host");
+    if (!rc)
+        rc = hip_err(hipStreamSynchronize(a->stream), "sync");
+    return rc;
+}
+
+extern "C" void janas_attn_forget(struct janas_attn *a, const void *p)
+{
+    if (!a || !p)
+        return;
+    const char *q = (const char *)p;
+    for (size_t i = 0; i < a->copies->size(); i++) {
+        HostCopy &c = (*a->copies)[i];
+        if (q >= c.host && q < c.host + c.bytes) {
+            (void)hipSetDevice(a->dev);
+            (void)hipStreamSynchronize(a->stream);
+            (void)hipFree(c.dev);
+            a->copies->erase(a->copies->begin() + i);
+            return;
+        }
+    }
 }
 
 /* ===== Part 2 ========================================================= */

@@ -151,3 +151,14 @@ int main(void)
     pb, rp = (int(x) for x in r.stdout.split())
     assert pb == 8 * 4 * janas_amd.MAX_BLOCK * 4 * 130 * 4
     assert rp == (4096 + 64 + 256 + 255) // 256 * 256
+
+
+def test_import_entry_points_reject_null_without_a_device():
+    """janas_attn_import / _sync refuse a null instance, pointer or size
+    before any device call; janas_attn_forget of nothing is a no-op."""
+    L = lib()
+    buf = ctypes.create_string_buffer(64)
+    addr = ctypes.addressof(buf)
+    assert L.janas_attn_import(None, addr, 64) == janas_amd.EINVAL
+    assert L.janas_attn_sync(None, addr, 64, 1) == janas_amd.EINVAL
+    L.janas_attn_forget(None, addr)

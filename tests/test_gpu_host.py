@@ -129,3 +129,126 @@ def test_run_returns_instead_of_abort(gpu):
         assert within(abs_err(out, ref), TOL_FLOAT_ABS, "abs_err(out, ref)")
         a.clear_status()
         assert a.status() == 0
+
+
+def imported_case(kv_dtype, n_kv=2, h=8, hd=128, n_ctx=1024, seed=61):
+    k, ks = int_cache(seed, n_kv, n_ctx, hd, kv_dtype)
+    v, vs = int_cache(seed + 2, n_kv, n_ctx, hd, kv_dtype)
+    return k, ks, v, vs
+
+
+def staged(h, n_kv, hd, n_ctx, kv16, ring, q, k, ks, v, vs, n, pos0):
+    """The same call through the staging path (nothing imported)."""
+    out = np.zeros_like(q)
+    with Attention(h, n_kv, hd, n_ctx, 1, janas_amd.FLOAT) as a:
+        a.set_kv16(kv16)
+        a.set_ring(ring)
+        a.run(q, k, ks, v, vs, n, pos0, out)
+        assert a.status() == 0
+    return out
+
+
+@pytest.mark.parametrize("kv16", [False, True])
+def test_imported_cache_equals_staging(kv16, gpu):
+    """janas_attn_run over an imported host cache (janas_attn_import) reads
+    the device copy: a decode and a 64-token block equal the staging path
+    bit for bit and the oracle within the FLOAT bar; the rows of a call's
+    positions are taken from the host at the call (the engine writes them
+    just before), a change anywhere else is not seen until janas_attn_sync,
+    and after janas_attn_forget the call stages the host cache again."""
+    h, n_kv, hd, n_ctx = 8, 2, 128, 1024
+    dt = np.int16 if kv16 else np.int8
+    kvt = orc.KV_I16 if kv16 else orc.KV_I8
+    k, ks, v, vs = imported_case(dt)
+    q1 = normal(71, h * hd).reshape(1, h, hd)
+    q64 = normal(73, 64 * h * hd).reshape(64, h, hd)
+    with Attention(h, n_kv, hd, n_ctx, 1, janas_amd.FLOAT) as a:
+        a.set_kv16(kv16)
+        for arr in (k, ks, v, vs):
+            assert a.import_host(arr) == 0
+        assert a.import_host(k[1]) == 0          # inside an import: nothing new
+        # a decode at 700 and a block at 900..963
+        for q, n, pos0 in ((q1, 1, 700), (q64, 64, 900)):
+            out = np.zeros_like(q)
+            a.run(q, k, ks, v, vs, n, pos0, out)
+            assert a.status() == 0
+            ref_st = staged(h, n_kv, hd, n_ctx, kv16, False, q, k, ks, v, vs, n, pos0)
+            assert np.array_equal(out.view(np.int32), ref_st.view(np.int32))
+            ref = reference(q, k, ks, v, vs, kvt, pos0, h, n_kv, hd)
+            assert within(abs_err(out, ref), TOL_FLOAT_ABS, f"imported n={n} vs oracle")
+        # the engine writes the next block's rows 964..1003, then calls
+        rng = np.random.default_rng(5)
+        k[:, 964:1004] = rng.integers(-100, 100, (n_kv, 40, hd)).astype(dt)
+        vs[:, 964:1004] *= np.float32(1.5)
+        q40 = normal(79, 40 * h * hd).reshape(40, h, hd)
+        out = np.zeros_like(q40)
+        a.run(q40, k, ks, v, vs, 40, 964, out)
+        ref_st = staged(h, n_kv, hd, n_ctx, kv16, False, q40, k, ks, v, vs, 40, 964)
+        assert np.array_equal(out.view(np.int32), ref_st.view(np.int32))
+        # a change before pos0 is the caller's to sync
+        old = staged(h, n_kv, hd, n_ctx, kv16, False, q1, k, ks, v, vs, 1, 1003)
+        k[:, 100:110] = -k[:, 100:110]
+        new = staged(h, n_kv, hd, n_ctx, kv16, False, q1, k, ks, v, vs, 1, 1003)
+        assert not np.array_equal(old, new)
+        out = np.zeros_like(q1)
+        a.run(q1, k, ks, v, vs, 1, 1003, out)
+        assert np.array_equal(out.view(np.int32), old.view(np.int32))
+        assert a.sync(k) == 0
+        a.run(q1, k, ks, v, vs, 1, 1003, out)
+        assert np.array_equal(out.view(np.int32), new.view(np.int32))
+        # the device copy back to the host
+        k_dev_view = k.copy()
+        k[:] = 0
+        assert a.sync(k, to_device=False) == 0
+        assert np.array_equal(k, k_dev_view)
+        # forgotten: staged again, so a host change is seen at once
+        a.forget(k)
+        k[:, 200:210] = -k[:, 200:210]
+        after = staged(h, n_kv, hd, n_ctx, kv16, False, q1, k, ks, v, vs, 1, 1003)
+        a.run(q1, k, ks, v, vs, 1, 1003, out)
+        assert np.array_equal(out.view(np.int32), after.view(np.int32))
+        assert a.status() == 0
+
+
+def test_imported_ring_cache_takes_wrapped_rows(gpu):
+    """A ring (position p in row p mod n_ctx, window 200): a block at
+    positions 480..543 writes rows 480..511 and 0..31, and the call over the
+    imported cache takes both runs from the host."""
+    h, n_kv, hd, n_ctx, window = 8, 2, 128, 512, 200
+    k, ks, v, vs = imported_case(np.int8, n_ctx=n_ctx, seed=91)
+    q = normal(93, 64 * h * hd).reshape(64, h, hd)
+    with Attention(h, n_kv, hd, n_ctx, 1, janas_amd.FLOAT) as a:
+        a.set_ring(True)
+        a.set_window(window)
+        for arr in (k, ks, v, vs):
+            assert a.import_host(arr) == 0
+        rng = np.random.default_rng(9)
+        for rows in (slice(480, 512), slice(0, 32)):
+            k[:, rows] = rng.integers(-120, 120, (n_kv, 32, hd)).astype(np.int8)
+            v[:, rows] = rng.integers(-120, 120, (n_kv, 32, hd)).astype(np.int8)
+            ks[:, rows] *= np.float32(0.5)
+        out = np.zeros_like(q)
+        a.run(q, k, ks, v, vs, 64, 480, out)
+        assert a.status() == 0
+    ref = np.zeros_like(q)
+    with Attention(h, n_kv, hd, n_ctx, 1, janas_amd.FLOAT) as b:
+        b.set_ring(True)
+        b.set_window(window)
+        b.run(q, k, ks, v, vs, 64, 480, ref)
+    assert np.array_equal(out.view(np.int32), ref.view(np.int32))
+
+
+def test_import_refuses_partial_overlap(gpu):
+    """An import that overlaps another in part is refused, one inside it is
+    a no-op, a sync outside every import is refused."""
+    h, n_kv, hd, n_ctx = 8, 2, 64, 256
+    buf = np.zeros(4096, np.int8)
+    with Attention(h, n_kv, hd, n_ctx, 1, janas_amd.FLOAT) as a:
+        assert a.import_host(buf[1024:3072]) == 0
+        assert a.import_host(buf[2048:4096]) == janas_amd.EINVAL
+        assert a.import_host(buf[1024:2048]) == 0
+        assert a.sync(buf[0:512]) == janas_amd.EINVAL
+        assert a.sync(buf[1500:1600]) == 0
+        a.forget(buf[1024:3072])
+        assert a.sync(buf[1500:1600]) == janas_amd.EINVAL
+        assert a.import_host(buf[2048:4096]) == 0
