@@ -85,6 +85,11 @@ struct janas_attn {
     std::vector<ProfEv> *ev_used, *ev_free;
     /* imported host ranges (janas_attn_import) */
     std::vector<HostCopy> *copies;
+    /* pinned host memory for what a janas_attn_run with host pointers
+       sends and receives besides a staged cache: q, the rows of imported
+       caches, out */
+    char *pin;
+    size_t pin_bytes;
 };
 
 namespace {
@@ -1150,6 +1155,7 @@ extern "C" void janas_attn_destroy(struct janas_attn *a)
             (void)hipFree(c.dev);
         delete a->copies;
     }
+    (void)hipHostFree(a->pin);
     for (std::vector<ProfEv> *v : {a->ev_used, a->ev_free})
         if (v) {
             for (ProfEv &ev : *v) {
@@ -1215,6 +1221,23 @@ namespace {
 
 /* A staging buffer of at least `need` bytes (the stream that used it is
    synchronized at the end of every janas_attn_run, so the old one is idle). */
+/* the instance's pinned host buffer, at least need bytes */
+bool pinned(janas_attn *a, size_t need)
+{
+    if (a->pin && a->pin_bytes >= need)
+        return true;
+    (void)hipHostFree(a->pin);
+    a->pin = nullptr;
+    a->pin_bytes = 0;
+    if (hipHostMalloc((void **)&a->pin, need, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        a->pin = nullptr;
+        return false;
+    }
+    a->pin_bytes = need;
+    return true;
+}
+
 bool staging(void **p, size_t *have, size_t need)
 {
     if (*p && *have >= need)
@@ -1237,6 +1260,9 @@ bool staging(void **p, size_t *have, size_t need)
 void run_failed(janas_attn *a, const char *what, int rc, float *out, size_t qbytes,
                 bool out_host)
 {
+    /* nothing of this call may still read or write the pinned buffer when
+       the next call fills it */
+    (void)hipStreamSynchronize(a->stream);
     note(a, rc);
     if (a->abort_on_error)
         die(what, rc);
@@ -1299,19 +1325,52 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
     const size_t blk_bytes =
         (size_t)JANAS_ATTN_MAX_BLOCK * a->n_head * hd * sizeof(float);
     size_t have_q = a->st_q ? blk_bytes : 0, have_out = a->st_out ? blk_bytes : 0;
-    if (is_device_ptr(q)) {
+    /* the cache: in place on the device, an imported copy, else the rows
+       this call reads staged (the staging buffers follow the element size:
+       set_kv16 may change it) */
+    const size_t rows_all = (size_t)a->n_kv * cap;
+    const size_t kv_bytes = rows_all * hd * eb, sc_bytes = rows_all * 4;
+    struct Src {
+        const void *p;
+        void **st;
+        size_t *have;
+        size_t bytes, esz;
+        const void **dst;
+        const HostCopy *copy;
+    } src[4] = {{k, &a->st_k, &a->st_k_bytes, kv_bytes, hd * eb, &s.k, nullptr},
+                {v, &a->st_v, &a->st_v_bytes, kv_bytes, hd * eb, &s.v, nullptr},
+                {ks, (void **)&a->st_ks, &a->st_ks_bytes, sc_bytes, 4, (const void **)&s.ks,
+                 nullptr},
+                {vs, (void **)&a->st_vs, &a->st_vs_bytes, sc_bytes, 4, (const void **)&s.vs,
+                 nullptr}};
+    /* pinned memory: q, the imported caches' rows of this call's positions
+       (pos0 .. end - 1, at most a ring's capacity), out */
+    const bool q_host = !is_device_ptr(q);
+    const size_t fresh = std::min<size_t>(end - pos0, cap);
+    size_t pin_need = (q_host ? (qbytes + 15) / 16 * 16 : 0) + (out_host ? qbytes : 0);
+    for (Src &x : src)
+        if (!is_device_ptr(x.p) && (x.copy = find_copy(a, x.p, x.bytes)))
+            pin_need += (a->n_kv * fresh * x.esz + 15) / 16 * 16;
+    if (pin_need && !pinned(a, pin_need)) {
+        run_failed(a, "pinned host memory", JANAS_ATTN_ENOMEM, out, qbytes, out_host);
+        return;
+    }
+    size_t pin_at = 0;
+    if (!q_host) {
         s.q = q;
     } else {
         if (!staging((void **)&a->st_q, &have_q, blk_bytes)) {
             run_failed(a, "staging q", JANAS_ATTN_ENOMEM, out, qbytes, out_host);
             return;
         }
-        rc = hip_err(hipMemcpyAsync(a->st_q, q, qbytes, hipMemcpyHostToDevice, a->stream),
+        memcpy(a->pin, q, qbytes);
+        rc = hip_err(hipMemcpyAsync(a->st_q, a->pin, qbytes, hipMemcpyHostToDevice, a->stream),
                      "copy q");
         if (rc) {
             run_failed(a, "staging q", rc, out, qbytes, out_host);
             return;
         }
+        pin_at = (qbytes + 15) / 16 * 16;
         s.q = a->st_q;
     }
     if (out_host) {
@@ -1323,37 +1382,52 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
     } else {
         s.out = out;
     }
-    /* the cache: in place on the device, else the rows this call reads (the
-       staging buffers follow the element size: set_kv16 may change it) */
-    const size_t rows_all = (size_t)a->n_kv * cap;
-    const size_t kv_bytes = rows_all * hd * eb, sc_bytes = rows_all * 4;
     size_t r_lo = a->ring ? 0 : (size_t)c0 * kChunk;
     size_t r_hi = a->ring ? cap : end;
-    struct Src {
-        const void *p;
-        void **st;
-        size_t *have;
-        size_t bytes, esz;
-        const void **dst;
-    } src[4] = {{k, &a->st_k, &a->st_k_bytes, kv_bytes, hd * eb, &s.k},
-                {v, &a->st_v, &a->st_v_bytes, kv_bytes, hd * eb, &s.v},
-                {ks, (void **)&a->st_ks, &a->st_ks_bytes, sc_bytes, 4, (const void **)&s.ks},
-                {vs, (void **)&a->st_vs, &a->st_vs_bytes, sc_bytes, 4, (const void **)&s.vs}};
+    RefreshArgs ra;
+    memset(&ra, 0, sizeof ra);
+    ra.n_kv = a->n_kv;
+    ra.cap = (uint32_t)cap;
+    ra.lo = (uint32_t)(a->ring ? pos0 % cap : pos0);
+    ra.count = (uint32_t)fresh;
     for (Src &x : src) {
-        if (is_device_ptr(x.p)) {
-            *x.dst = x.p;
-            continue;
-        }
-        if (const HostCopy *c = find_copy(a, x.p, x.bytes)) {
-            /* an imported cache: its device copy, with the rows of this
-               call's positions taken from the host first */
+        if (x.copy) {
+            /* an imported cache: its device copy, the rows of this call's
+               positions taken from the host first - packed into pinned
+               memory and put in place by one kernel for all four arrays,
+               or by 2D copies where a row is not whole 4-byte words */
+            const HostCopy *c = x.copy;
             char *dev = c->dev + ((const char *)x.p - c->host);
-            rc = refresh_rows(a, dev, x.p, x.esz, pos0, end);
-            if (rc) {
-                run_failed(a, "the imported cache", rc, out, qbytes, out_host);
-                return;
+            if ((uintptr_t)dev % 4 || (uintptr_t)x.p % 4 || x.esz % 4) {
+                rc = refresh_rows(a, dev, x.p, x.esz, pos0, end);
+                if (rc) {
+                    run_failed(a, "the imported cache", rc, out, qbytes, out_host);
+                    return;
+                }
+            } else {
+                char *dst = a->pin + pin_at;
+                for (uint32_t h = 0; h < a->n_kv; h++) {
+                    size_t lo = ra.lo, left = fresh;
+                    while (left) {
+                        const size_t run = std::min(left, cap - lo);
+                        memcpy(dst, (const char *)x.p + ((size_t)h * cap + lo) * x.esz,
+                               run * x.esz);
+                        dst += run * x.esz;
+                        left -= run;
+                        lo = 0;
+                    }
+                }
+                ra.src[ra.n_t] = (const uint32_t *)(a->pin + pin_at);
+                ra.dst[ra.n_t] = (uint32_t *)dev;
+                ra.words[ra.n_t] = (uint32_t)(x.esz / 4);
+                ra.n_t++;
+                pin_at += (a->n_kv * fresh * x.esz + 15) / 16 * 16;
             }
             *x.dst = dev;
+            continue;
+        }
+        if (is_device_ptr(x.p)) {
+            *x.dst = x.p;
             continue;
         }
         if (!staging(x.st, x.have, x.bytes)) {
@@ -1389,6 +1463,13 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
         s.last = a->st_last;
         s.last_max = last[n - 1];
     }
+    if (ra.n_t) {
+        rc = hip_err(launch_refresh(ra, a->stream), "the imported cache's rows");
+        if (rc) {
+            run_failed(a, "the imported cache", rc, out, qbytes, out_host);
+            return;
+        }
+    }
     choose_way(a, kv, n, pos0);
     rc = run_split(a, kv, kGateNone, &s, 1, a->stream);
     if (rc) {
@@ -1396,8 +1477,9 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
         run_failed(a, "attention", rc, out, qbytes, out_host);
         return;
     }
+    char *pin_out = out_host ? a->pin + pin_at : nullptr;
     if (out_host) {
-        rc = hip_err(hipMemcpyAsync(out, a->st_out, qbytes, hipMemcpyDeviceToHost, a->stream),
+        rc = hip_err(hipMemcpyAsync(pin_out, a->st_out, qbytes, hipMemcpyDeviceToHost, a->stream),
                      "copy out");
         if (rc) {
             (void)hipStreamSynchronize(a->stream);
@@ -1406,8 +1488,12 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
         }
     }
     rc = hip_err(hipStreamSynchronize(a->stream), "synchronize");
-    if (rc)
+    if (rc) {
         run_failed(a, "synchronize", rc, out, qbytes, out_host);
+        return;
+    }
+    if (out_host)
+        memcpy(out, pin_out, qbytes);
 }
 
 extern "C" int janas_attn_status(const struct janas_attn *a)

@@ -228,7 +228,34 @@ __global__ __launch_bounds__(256) void q8k_kernel(const Q8kArgs A)
     q8k_block(A.x[(size_t)b * 256 + t], t, A.y + (size_t)b * kQ8kBytes, S);
 }
 
+/* one 4-byte word a thread: tensor blockIdx.y, word i of its packed rows */
+__global__ __launch_bounds__(256) void refresh_kernel(const RefreshArgs A)
+{
+    const uint32_t t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t w = A.words[t], per_head = A.count * w;
+    if (i >= A.n_kv * per_head)
+        return;
+    const uint32_t h = i / per_head, r = (i % per_head) / w, e = i % w;
+    const uint32_t row = (A.lo + r) % A.cap;
+    A.dst[t][((size_t)h * A.cap + row) * w + e] = A.src[t][i];
+}
+
 }  // namespace
+
+hipError_t launch_refresh(const RefreshArgs &a, hipStream_t s)
+{
+    uint32_t most = 0;
+    for (uint32_t t = 0; t < a.n_t; t++)
+        most = a.words[t] > most ? a.words[t] : most;
+    const uint64_t words = (uint64_t)a.n_kv * a.count * most;
+    if (a.n_t == 0 || words == 0)
+        return hipSuccess;
+    if (a.n_t > 4 || words > 0xFFFFFFFFull)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(refresh_kernel, dim3((uint32_t)((words + 255) / 256), a.n_t), dim3(256),
+                       0, s, a);
+    return hipGetLastError();
+}
 
 hipError_t launch_rows(const RowArgs &a, hipStream_t s)
 {

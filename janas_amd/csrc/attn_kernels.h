@@ -180,7 +180,20 @@ uint32_t split_mt(int kv, uint32_t hd, uint32_t tiles);
    caches); launch_split hands those to it. */
 hipError_t launch_wide(int kv, const SplitArgs &a, hipStream_t s);
 
+/* Rows of imported host caches a janas_attn_run takes (attn_cache.hip):
+   for tensor t (keys, values, their scales), rows lo, lo + 1, .. (mod cap)
+   of every KV head, count of them, packed [head][row] in pinned host memory
+   at src[t], into the device copy dst[t] ([n_kv][cap] rows of words[t]
+   4-byte words). */
+struct RefreshArgs {
+    const uint32_t *src[4];
+    uint32_t *dst[4];
+    uint32_t words[4];
+    uint32_t n_t, n_kv, cap, lo, count;
+};
+
 /* attn_cache.hip */
+hipError_t launch_refresh(const RefreshArgs &a, hipStream_t s);
 hipError_t launch_rows(const RowArgs &a, hipStream_t s);
 hipError_t launch_shift(const ShiftArgs &a, hipStream_t s);
 hipError_t launch_q8k(const Q8kArgs &a, hipStream_t s);
