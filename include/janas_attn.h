@@ -8,8 +8,9 @@
  * and values n_head_kv x n_ctx x head_dim signed bytes (sixteen-bit with
  * janas_attn_set_kv16), one float scale per (KV head, position), position p
  * in row p (or p mod n_ctx in a ring). Pointers may be device memory (used
- * in place) or host memory (staged through the device each call; correct,
- * but bounded by PCIe - keep the cache in device memory).
+ * in place) or host memory: a host cache is staged through the device each
+ * call (correct, but bounded by PCIe), unless it was imported
+ * (janas_attn_import), when only the rows of the call's positions cross.
  *
  * Part 2 extends it for callers that keep everything on the device: f16
  * and f32 caches besides int8 / int16, any number of tokens a call, several
