@@ -141,7 +141,8 @@ def cpu_model():
 
 
 def cpu_cores():
-    """Every core the host gives this process (all host cores)."""
+    """Every core the host gives this process: the CPU baseline runs the
+    restatement on all of them."""
     try:
         return max(1, len(os.sched_getaffinity(0)))
     except AttributeError:

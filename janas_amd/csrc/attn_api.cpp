@@ -64,9 +64,9 @@ struct janas_attn {
        once it is done */
     hipStream_t part_stream;
     hipEvent_t part_ev;
-    /* f16 copies of an int8 / int16 cache's keys and values for long
-       prompts (dequant_bytes each), ordered across streams as the
-       partials */
+    /* the exact prefill kernel's copies of an int8 / int16 cache's keys
+       and values as f16 planes (dq_bytes each), ordered across streams as
+       the partials */
     void *dq_k, *dq_v;
     size_t dq_bytes;
     /* staging of host pointers for janas_attn_run, and the bytes each
