@@ -114,6 +114,27 @@ template <> struct Elem<kI8> {
     }
 };
 
+/* 4 int16 numbers (two words, the first in the low half) as the f16 planes
+   256 (x >> 8) and x & 255, both exact. A byte under the exponent byte 0x64
+   is the half 1024 + b (halves in [1024, 2048) step by 1): the low bytes
+   less 1024 are x & 255; the high bytes, flipped to b + 128, less 1152 are
+   x >> 8, times 256 - two byte permutes and six packed f16 operations for
+   the 4, the same numbers as converting each through f32 */
+__device__ __forceinline__ void i16_planes4(uint32_t w0, uint32_t w1, h4 &hi, h4 &lo)
+{
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const h2 k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2 k256 = {(_Float16)256.0f, (_Float16)256.0f};
+    const h2 l0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w0, 0x04020400u)) - k1024;
+    const h2 l1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w1, 0x04020400u)) - k1024;
+    const h2 h0 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w0 ^ 0x80808080u,
+                                                                0x04030401u)) - k1152) * k256;
+    const h2 h1 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w1 ^ 0x80808080u,
+                                                                0x04030401u)) - k1152) * k256;
+    lo = h4{l0[0], l0[1], l1[0], l1[1]};
+    hi = h4{h0[0], h0[1], h1[0], h1[1]};
+}
+
 template <> struct Elem<kI16> {
     static constexpr int bytes = 2, planes = 2;
     struct Raw { uint4 a; };
@@ -124,13 +145,11 @@ template <> struct Elem<kI16> {
     /* x = 256 (x >> 8) + (x & 255): both parts exact in f16 */
     __device__ static void split(uint4 u, h8 &hi, h8 &lo)
     {
-        uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            int x = (int)(int16_t)(w[e / 2] >> (16 * (e % 2)));
-            hi[e] = (_Float16)(float)((x >> 8) * 256);
-            lo[e] = (_Float16)(x & 255);
-        }
+        h4 h0, h1, l0, l1;
+        i16_planes4(u.x, u.y, h0, l0);
+        i16_planes4(u.z, u.w, h1, l1);
+        hi = h8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+        lo = h8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
     }
     __device__ static void planes8(const Raw &r, h8 *p) { split(r.a, p[0], p[1]); }
 };

@@ -600,13 +600,7 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
             if constexpr (T == kI16) {
                 const h4 x = lds_read_tr((const _Float16 *)(myR + a));
                 const uint2 u = __builtin_bit_cast(uint2, x);
-                const uint32_t wv[2] = {u.x, u.y};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int xi = (int)(int16_t)(wv[e / 2] >> (16 * (e % 2)));
-                    vb[t][0][e] = (_Float16)(float)((xi >> 8) * 256);
-                    vb[t][1][e] = (_Float16)(xi & 255);
-                }
+                i16_planes4(u.x, u.y, vb[t][0], vb[t][1]);
             } else {
                 vb[t][0] = lds_read_tr((const _Float16 *)(myR + a));
                 if constexpr (T == kF32)

@@ -69,13 +69,8 @@ __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c)
 /* four int16 (as halves' bits) -> exact f16 planes 256 (x >> 8), x & 255 */
 __device__ __forceinline__ void split16(h4 raw, h4 &hi, h4 &lo)
 {
-    const s4 v = __builtin_bit_cast(s4, raw);
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const int x = v[e];
-        hi[e] = (_Float16)(float)((x >> 8) * 256);
-        lo[e] = (_Float16)(x & 255);
-    }
+    const uint2 u = __builtin_bit_cast(uint2, raw);
+    i16_planes4(u.x, u.y, hi, lo);
 }
 
 template <int T, int D> struct WShape {
