@@ -13,13 +13,11 @@
 #include <hip/hip_runtime.h>
 
 #include "attn_kernels.h"
+#include "attn_planes.h"
 
 namespace janas {
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef short s4 __attribute__((ext_vector_type(4)));
 /* 16 bytes as a native vector (HIP's uint4 is a struct, which keeps large
@@ -88,52 +86,13 @@ template <> struct Elem<kI8> {
     {
         return Raw{*(const uint2 *)((const int8_t *)b + i)};
     }
-    /* 4 signed bytes to 4 halves, exactly: byte b ^ 0x80 = b + 128 as the
-       low mantissa byte under the high byte 0x64 is the half 1024 + b +
-       128 (halves in [1024, 2048) step by 1), less 1152 is b - one xor,
-       two byte permutes and two packed adds for 4 numbers */
-    __device__ static void widen4(uint32_t x, h2 &a, h2 &b)
-    {
-        const uint32_t u = x ^ 0x80808080u;
-        const uint32_t pa = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
-        const uint32_t pb = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
-        const h2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
-        a = __builtin_bit_cast(h2, pa) - off;
-        b = __builtin_bit_cast(h2, pb) - off;
-    }
-    __device__ static h8 widen(uint32_t lo, uint32_t hi)
-    {
-        h2 p[4];
-        widen4(lo, p[0], p[1]);
-        widen4(hi, p[2], p[3]);
-        return h8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
-    }
+    /* 8 signed bytes to 8 halves, exactly (i8_widen8) */
+    __device__ static h8 widen(uint32_t lo, uint32_t hi) { return i8_widen8(lo, hi); }
     __device__ static void planes8(const Raw &r, h8 *p)
     {
         p[0] = widen(r.a.x, r.a.y);
     }
 };
-
-/* 4 int16 numbers (two words, the first in the low half) as the f16 planes
-   256 (x >> 8) and x & 255, both exact. A byte under the exponent byte 0x64
-   is the half 1024 + b (halves in [1024, 2048) step by 1): the low bytes
-   less 1024 are x & 255; the high bytes, flipped to b + 128, less 1152 are
-   x >> 8, times 256 - two byte permutes and six packed f16 operations for
-   the 4, the same numbers as converting each through f32 */
-__device__ __forceinline__ void i16_planes4(uint32_t w0, uint32_t w1, h4 &hi, h4 &lo)
-{
-    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-    const h2 k1152 = {(_Float16)1152.0f, (_Float16)1152.0f};
-    const h2 k256 = {(_Float16)256.0f, (_Float16)256.0f};
-    const h2 l0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w0, 0x04020400u)) - k1024;
-    const h2 l1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w1, 0x04020400u)) - k1024;
-    const h2 h0 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w0 ^ 0x80808080u,
-                                                                0x04030401u)) - k1152) * k256;
-    const h2 h1 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w1 ^ 0x80808080u,
-                                                                0x04030401u)) - k1152) * k256;
-    lo = h4{l0[0], l0[1], l1[0], l1[1]};
-    hi = h4{h0[0], h0[1], h1[0], h1[1]};
-}
 
 template <> struct Elem<kI16> {
     static constexpr int bytes = 2, planes = 2;
@@ -143,14 +102,7 @@ template <> struct Elem<kI16> {
         return Raw{*(const uint4 *)((const int16_t *)b + i)};
     }
     /* x = 256 (x >> 8) + (x & 255): both parts exact in f16 */
-    __device__ static void split(uint4 u, h8 &hi, h8 &lo)
-    {
-        h4 h0, h1, l0, l1;
-        i16_planes4(u.x, u.y, h0, l0);
-        i16_planes4(u.z, u.w, h1, l1);
-        hi = h8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
-        lo = h8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
-    }
+    __device__ static void split(uint4 u, h8 &hi, h8 &lo) { i16_planes8(u.x, u.y, u.z, u.w, hi, lo); }
     __device__ static void planes8(const Raw &r, h8 *p) { split(r.a, p[0], p[1]); }
 };
 

@@ -69,14 +69,12 @@
 #include <hip/hip_runtime.h>
 
 #include "attn_kernels.h"
+#include "attn_planes.h"
 #include "attn_q8k.h"
 
 namespace janas {
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16x __attribute__((ext_vector_type(16)));
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
@@ -1448,29 +1446,15 @@ __global__ __launch_bounds__(256) void xcopy_kernel(const DqArgs A)
     if constexpr (T == kI8) {
         const uint2 kx = *(const uint2 *)((const char *)A.k + r * A.hd + cu * 8);
         const uint2 vx = *(const uint2 *)((const char *)A.v + r * A.hd + cu * 8);
-        h8 kh, vh;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            kh[e] = (_Float16)(int8_t)(kx.x >> (8 * e));
-            kh[4 + e] = (_Float16)(int8_t)(kx.y >> (8 * e));
-            vh[e] = (_Float16)(int8_t)(vx.x >> (8 * e));
-            vh[4 + e] = (_Float16)(int8_t)(vx.y >> (8 * e));
-        }
-        *(h8 *)(A.k16 + dst) = kh;
-        *(h8 *)(A.v16 + dst) = vh;
+        *(h8 *)(A.k16 + dst) = i8_widen8(kx.x, kx.y);
+        *(h8 *)(A.v16 + dst) = i8_widen8(vx.x, vx.y);
     } else {
+        /* x & ~255 = 256 (x >> 8), and x & 255 */
         const u4 kx = *(const u4 *)((const char *)A.k + 2 * (r * A.hd + cu * 8));
         const u4 vx = *(const u4 *)((const char *)A.v + 2 * (r * A.hd + cu * 8));
         h8 k0, k1, v0, v1;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int32_t a = (int16_t)(kx[e / 2] >> (16 * (e % 2)));
-            const int32_t b = (int16_t)(vx[e / 2] >> (16 * (e % 2)));
-            k0[e] = (_Float16)(a & ~255);
-            k1[e] = (_Float16)(a & 255);
-            v0[e] = (_Float16)(b & ~255);
-            v1[e] = (_Float16)(b & 255);
-        }
+        i16_planes8(kx[0], kx[1], kx[2], kx[3], k0, k1);
+        i16_planes8(vx[0], vx[1], vx[2], vx[3], v0, v1);
         *(h8 *)(A.k16 + dst) = k0;
         *(h8 *)(A.k16 + plane + dst) = k1;
         *(h8 *)(A.v16 + dst) = v0;
