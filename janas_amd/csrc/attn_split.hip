@@ -166,7 +166,8 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
     __shared__ __attribute__((aligned(16))) float sL[kSW][TR];
     __shared__ float sPe[kSW];
     __shared__ float sX[kSW][TR];   /* INT16: largest weight x value scale */
-    __shared__ float sKs[kSW][kSWP], sVs[kSW][kSWP];
+    __shared__ __attribute__((aligned(16))) float sKs[kSW][kSWP];
+    __shared__ __attribute__((aligned(16))) float sVs[kSW][kSWP];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t g = lane >> 4, l16 = lane & 15;
@@ -447,6 +448,12 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
                 for (int dp = 0; dp < DP; dp++)
                     sa[mt] = mfma(ka[dp], qb[mt][ks], sa[mt]);
         }
+        /* the key scales of the lane's 4 positions, one read for all of
+           them (read under the mask below, each was a branch and a wait of
+           its own) */
+        f4 kz = f4{1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (S::SCALED)
+            kz = *(const f4 *)&sKs[w][kSG * s + 4 * g];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
@@ -458,11 +465,11 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
                 const float other = from_x1(sa[mt][i]);
                 const bool odd = l16 & 1;
                 x = q16_score(odd ? other : sa[mt][i], odd ? sa[mt][i] : other, qsc[mt], A.scale,
-                              sKs[w][pl]);
+                              kz[i]);
             } else {
                 x = (sa[mt][i] + from_x1(sa[mt][i])) * qs2[mt];
                 if constexpr (S::SCALED)
-                    x *= sKs[w][pl];
+                    x *= kz[i];
             }
             sv[mt][s][i] = p >= rlo[mt] && p <= rhi[mt] ? x : -INFINITY;
             m[mt] = fmaxf(m[mt], sv[mt][s][i]);
@@ -471,6 +478,11 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
         m[mt] = max_x32(max_x16(m[mt]));
+    /* the value scales of the lane's 16 positions, in registers */
+    f4 vz[kSNG];
+#pragma unroll
+    for (int s = 0; s < kSNG; s++)
+        vz[s] = S::SCALED ? *(const f4 *)&sVs[w][kSG * s + 4 * g] : f4{1.0f, 1.0f, 1.0f, 1.0f};
     h4 pa[MT][kSNG];
     if constexpr (Q16) {
         /* INT16: the chunk's largest score over the 4 waves, the weights
@@ -496,7 +508,7 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
                 for (int i = 0; i < 4; i++) {
                     const float wt = det_weight(sv[mt][s][i], mm);
                     lsum += wt;
-                    pv[mt][s][i] = wt * sVs[w][kSG * s + 4 * g + i];
+                    pv[mt][s][i] = wt * vz[s][i];
                     vmx = fmaxf(vmx, pv[mt][s][i]);
                 }
             vmx = max_x32(max_x16(vmx));
@@ -530,7 +542,7 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
         for (int s = 0; s < kSNG; s++)
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                vm = fmaxf(vm, sVs[w][kSG * s + 4 * g + i]);
+                vm = fmaxf(vm, vz[s][i]);
         vm = max_x32(max_x16(vm));
         int ev = 0;
         if (vm > 0.0f && vm < INFINITY)
@@ -552,7 +564,7 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
                     lsum += pw;
                     float pv = pw * up;
                     if constexpr (S::SCALED)
-                        pv *= sVs[w][kSG * s + 4 * g + i];
+                        pv *= vz[s][i];
                     _Float16 hi, lo;
                     split_hl(pv, hi, lo);
                     pa[mt][s][i] = (l16 & 1) ? lo : hi;
