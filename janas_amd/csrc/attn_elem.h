@@ -202,6 +202,18 @@ __device__ __forceinline__ float sum_x32(float a)
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+/* the largest over each row of 16 lanes, in every lane of it: DPP
+   quad_perm [1, 0, 3, 2] and [2, 3, 0, 1], then row_ror 4 and 8 (a maximum
+   does not depend on the order it is taken in, so this is the same number
+   as lane-by-lane shuffles give, without their LDS round trips) */
+__device__ __forceinline__ float max_row16(float a)
+{
+    a = fmaxf(a, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(a), 0xB1, 0xf, 0xf, false)));
+    a = fmaxf(a, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(a), 0x4E, 0xf, 0xf, false)));
+    a = fmaxf(a, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(a), 0x124, 0xf, 0xf, false)));
+    a = fmaxf(a, __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(a), 0x128, 0xf, 0xf, false)));
+    return a;
+}
 /* lane l ^ 1's value (DPP quad_perm [1, 0, 3, 2]) */
 __device__ __forceinline__ float from_x1(float a)
 {

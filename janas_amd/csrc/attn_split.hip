@@ -312,9 +312,13 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
         float mx = 0.0f;
         if (ok && qcol[h] < hd)
             mx = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-#pragma unroll
-        for (int o2 = 1; o2 < QL; o2 <<= 1)
-            mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
+        /* over the row's QL lanes (16, 32 or 64) */
+        static_assert(QL == 16 || QL == 32 || QL == 64, "rows of whole 16-lane groups");
+        mx = max_row16(mx);
+        if constexpr (QL >= 32)
+            mx = max_x16(mx);
+        if constexpr (QL >= 64)
+            mx = max_x32(mx);
         if constexpr (Q16) {
             /* INT16: the row as int16 with one scale (quant_worker,
                attention.c:820-839), planes x >> 8 and x & 255 */

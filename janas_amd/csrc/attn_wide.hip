@@ -227,9 +227,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
             if (qok[i])
                 mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qv[i].x), fabsf(qv[i].y)),
                                      fmaxf(fabsf(qv[i].z), fabsf(qv[i].w))));
-#pragma unroll
-        for (int o2 = 1; o2 < 16; o2 <<= 1)
-            mx = fmaxf(mx, __shfl_xor(mx, o2, 64));
+        mx = max_row16(mx);
         if constexpr (Q16) {
             /* the row as int16 with one scale (quant_worker,
                attention.c:820-839): planes x >> 8 and x & 255 */
@@ -415,8 +413,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
                the chunk, and the weights quantized against it to
                0 .. 32767, planes w >> 8 and w & 255 (att_weights_ref,
                att_wquant_ref, attention.c:158-176, :574-588, :761-772) */
-            m = fmaxf(m, __shfl_xor(m, 16, 64));
-            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            m = max_x32(max_x16(m));
             if (lane < 16)
                 sMax[w][lane] = m;
             __syncthreads();
@@ -431,10 +428,8 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
                 pv[e] = wt * sVz[pl + kRound * (e / 4) + e % 4];
                 vmx = fmaxf(vmx, pv[e]);
             }
-            vmx = fmaxf(vmx, __shfl_xor(vmx, 16, 64));
-            vmx = fmaxf(vmx, __shfl_xor(vmx, 32, 64));
-            lsum += __shfl_xor(lsum, 16, 64);
-            lsum += __shfl_xor(lsum, 32, 64);
+            vmx = max_x32(max_x16(vmx));
+            lsum = sum_x32(sum_x16(lsum));
             if (lane < 16)
                 sX[w][lane] = vmx;
             __syncthreads();
@@ -447,8 +442,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
             }
         } else if constexpr (s == kRounds - 1) {
             /* the wave's softmax over its 64 positions, one shot */
-            m = fmaxf(m, __shfl_xor(m, 16, 64));
-            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            m = max_x32(max_x16(m));
             /* the weights' power of two: the largest (e^0 times the largest
                value scale of the wave's positions) lands in [2^12, 2^13) */
             float vsc[4 * kRounds];
@@ -460,8 +454,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 #pragma unroll
                 for (int e = 0; e < 4 * kRounds; e++)
                     vm = fmaxf(vm, vsc[e]);
-                vm = fmaxf(vm, __shfl_xor(vm, 16, 64));
-                vm = fmaxf(vm, __shfl_xor(vm, 32, 64));
+                vm = max_x32(max_x16(vm));
                 int ev = 0;
                 if (vm > 0.0f && vm < INFINITY)
                     frexpf(vm, &ev);
@@ -480,8 +473,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
                 pa[e / 4][0][e % 4] = hi;
                 pa[e / 4][1][e % 4] = lo;
             }
-            lsum += __shfl_xor(lsum, 16, 64);
-            lsum += __shfl_xor(lsum, 32, 64);
+            lsum = sum_x32(sum_x16(lsum));
         }
     };
     static_assert(2 * kRounds == 8, "eight steps");
