@@ -847,7 +847,14 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     } else {
         gv[0].x = *gsrc;
     }
-    const float gh = *hsrc;
+    /* the same for the per-head gate: its address is the same in every
+       lane, and the compiler would make it a scalar load, for which the
+       partials' loads then wait (their addresses need the scalar counter
+       at zero); an opaque zero offset keeps it a vector load like the
+       others */
+    uint32_t z0;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z0));
+    const float gh = hsrc[z0];
     float mg = -INFINITY, lg = 0.0f;
     float4 ag[NV];
 #pragma unroll
