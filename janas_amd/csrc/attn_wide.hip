@@ -108,7 +108,8 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
                   "a round of V rows and half the sums fit the region");
     __shared__ __attribute__((aligned(16))) char sW[kWWaves * S::REGION];
     __shared__ __attribute__((aligned(16))) _Float16 sQ[2][kRows][S::QP];
-    __shared__ float sKz[kChunk], sVz[kChunk];
+    __shared__ __attribute__((aligned(16))) float sKz[kChunk];
+    __shared__ __attribute__((aligned(16))) float sVz[kChunk];
     __shared__ float sMax[kWWaves][kRows], sSum[kWWaves][kRows];
     __shared__ float sQs[kRows];
     __shared__ float sX[kWWaves][kRows];  /* INT16: largest weight x value scale */
@@ -356,6 +357,11 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
             const f4 acc = (sa[0][0] + sa[1][0]) + (sa[0][1] + sa[1][1]);
             /* INT16: the planes' exact sums apart */
             const f4 ahi = sa[0][0] + sa[1][0], alo = sa[0][1] + sa[1][1];
+            /* the key scales of the lane's 4 positions, one read (read
+               under the mask, each was a branch and a wait of its own) */
+            f4 kz = f4{1.0f, 1.0f, 1.0f, 1.0f};
+            if constexpr (S::SCALED)
+                kz = *(const f4 *)&sKz[pl + kRound * s];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t pc = pl + kRound * s + i; /* chunk-relative */
@@ -363,11 +369,11 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
                 float x = -INFINITY;
                 if (active && p >= rlo && p <= rhi && p <= plast) {
                     if constexpr (Q16) {
-                        x = q16_score(ahi[i], alo[i], qsc, A.scale, sKz[pc]);
+                        x = q16_score(ahi[i], alo[i], qsc, A.scale, kz[i]);
                     } else {
                         x = acc[i] * qs;
                         if constexpr (S::SCALED)
-                            x *= sKz[pc];
+                            x *= kz[i];
                     }
                 }
                 sv[4 * s + i] = x;
@@ -421,11 +427,15 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
             const float mm = m == -INFINITY ? 0.0f : m;
             float pv[4 * kRounds];
             float vmx = 0.0f;
+            f4 vz[kRounds];
+#pragma unroll
+            for (int r = 0; r < kRounds; r++)
+                vz[r] = *(const f4 *)&sVz[pl + kRound * r];
 #pragma unroll
             for (int e = 0; e < 4 * kRounds; e++) {
                 const float wt = det_weight(sv[e], mm);
                 lsum += wt;
-                pv[e] = wt * sVz[pl + kRound * (e / 4) + e % 4];
+                pv[e] = wt * vz[e / 4][e % 4];
                 vmx = fmaxf(vmx, pv[e]);
             }
             vmx = max_x32(max_x16(vmx));
@@ -447,8 +457,12 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
                value scale of the wave's positions) lands in [2^12, 2^13) */
             float vsc[4 * kRounds];
 #pragma unroll
-            for (int e = 0; e < 4 * kRounds; e++)
-                vsc[e] = S::SCALED ? sVz[pl + kRound * (e / 4) + e % 4] : 1.0f;
+            for (int r = 0; r < kRounds; r++) {
+                const f4 z = S::SCALED ? *(const f4 *)&sVz[pl + kRound * r] : f4{1.0f, 1.0f, 1.0f, 1.0f};
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    vsc[4 * r + i] = z[i];
+            }
             if constexpr (S::SCALED) {
                 float vm = 0.0f;
 #pragma unroll
