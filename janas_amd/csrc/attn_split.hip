@@ -982,10 +982,15 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 template <int T, int D, bool Q16, int MT>
 hipError_t launch_m(const SplitArgs &a, hipStream_t s)
 {
-    if (a.once && a.n_seqs == 1)
+    /* one sequence: its descriptor with the first arguments (a verify or a
+       64-token block 3 % faster than reading it after the count) */
+    const bool one = a.n_seqs == 1;
+    if (a.once && one)
         hipLaunchKernelGGL((split_kernel<T, D, true, true, Q16, MT>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
     else if (a.once)
         hipLaunchKernelGGL((split_kernel<T, D, true, false, Q16, MT>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
+    else if (one)
+        hipLaunchKernelGGL((split_kernel<T, D, false, true, Q16, MT>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
     else
         hipLaunchKernelGGL((split_kernel<T, D, false, false, Q16, MT>), dim3(a.n_wg), dim3(kSW * 64), 0, s, a);
     return hipGetLastError();
