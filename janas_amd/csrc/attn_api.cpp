@@ -1337,20 +1337,23 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
         size_t bytes, esz;
         const void **dst;
         const HostCopy *copy;
-    } src[4] = {{k, &a->st_k, &a->st_k_bytes, kv_bytes, hd * eb, &s.k, nullptr},
-                {v, &a->st_v, &a->st_v_bytes, kv_bytes, hd * eb, &s.v, nullptr},
+        bool dev;              /* device memory (asked once a call) */
+    } src[4] = {{k, &a->st_k, &a->st_k_bytes, kv_bytes, hd * eb, &s.k, nullptr, false},
+                {v, &a->st_v, &a->st_v_bytes, kv_bytes, hd * eb, &s.v, nullptr, false},
                 {ks, (void **)&a->st_ks, &a->st_ks_bytes, sc_bytes, 4, (const void **)&s.ks,
-                 nullptr},
+                 nullptr, false},
                 {vs, (void **)&a->st_vs, &a->st_vs_bytes, sc_bytes, 4, (const void **)&s.vs,
-                 nullptr}};
+                 nullptr, false}};
     /* pinned memory: q, the imported caches' rows of this call's positions
        (pos0 .. end - 1, at most a ring's capacity), out */
     const bool q_host = !is_device_ptr(q);
     const size_t fresh = std::min<size_t>(end - pos0, cap);
     size_t pin_need = (q_host ? (qbytes + 15) / 16 * 16 : 0) + (out_host ? qbytes : 0);
-    for (Src &x : src)
-        if (!is_device_ptr(x.p) && (x.copy = find_copy(a, x.p, x.bytes)))
+    for (Src &x : src) {
+        x.dev = is_device_ptr(x.p);
+        if (!x.dev && (x.copy = find_copy(a, x.p, x.bytes)))
             pin_need += (a->n_kv * fresh * x.esz + 15) / 16 * 16;
+    }
     if (pin_need && !pinned(a, pin_need)) {
         run_failed(a, "pinned host memory", JANAS_ATTN_ENOMEM, out, qbytes, out_host);
         return;
@@ -1426,7 +1429,7 @@ extern "C" void janas_attn_run(struct janas_attn *a, struct janas_pool *pool,
             *x.dst = dev;
             continue;
         }
-        if (is_device_ptr(x.p)) {
+        if (x.dev) {
             *x.dst = x.p;
             continue;
         }
