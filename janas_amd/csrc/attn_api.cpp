@@ -944,7 +944,7 @@ int run_prefill_x(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *se
     const int ex = kv == kI16 ? 2 : 1;
     for (uint32_t s0 = 0; s0 < n_seqs; s0 += kMaxSeqs) {
         const uint32_t m = std::min(kMaxSeqs, n_seqs - s0);
-        DqArgs q[kMaxSeqs];
+        XcopyArgs q[kMaxSeqs];
         size_t off[kMaxSeqs], total = 0;
         for (uint32_t i = 0; i < m; i++) {
             const janas_attn_seq &s = seqs[s0 + i];

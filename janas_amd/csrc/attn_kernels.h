@@ -105,7 +105,7 @@ struct PrefillArgs {
 /* An int8 / int16 cache's rows of positions p0 .. p0 + np - 1 as the
    exact kernel's f16 planes (xcopy_kernel): plane by plane, row
    kvh np + (p - p0) of each. */
-struct DqArgs {
+struct XcopyArgs {
     const void *k, *v;     /* the cache, [n_kv][cap][hd] */
     _Float16 *k16, *v16;   /* the copies, [planes][n_kv][np][hd] */
     uint32_t n_kv, cap, hd, ring;
@@ -219,7 +219,7 @@ int prefill_halves_supported(int kv, uint32_t hd);
    p0 .. p0 + np - 1, per KV head from p0, as 1 (int8) or 2 (int16) planes
    of n_kv x np x hd f16 each; k16 and v16 hold the planes one after the
    other */
-hipError_t launch_xcopy(int kv, const DqArgs &a, hipStream_t s);
+hipError_t launch_xcopy(int kv, const XcopyArgs &a, hipStream_t s);
 /* the ordered merge of split sequences' segment partials: a thread takes 4
    columns of one row (a row is one (token, head)), a workgroup
    kPMergeThreads of them; a sequence of n tokens takes pmerge_groups of

@@ -1435,7 +1435,7 @@ __global__ __launch_bounds__((PCfg<D, false, (T == kI16 ? 2 : 1)>::W) * 64) void
  * mod cap on a ring). A thread takes 8 numbers of one row.
  */
 template <int T>
-__global__ __launch_bounds__(256) void xcopy_kernel(const DqArgs A)
+__global__ __launch_bounds__(256) void xcopy_kernel(const XcopyArgs A)
 {
     const uint32_t upr = A.hd / 8;
     const uint64_t u = (uint64_t)blockIdx.x * 256 + threadIdx.x;
@@ -1808,7 +1808,7 @@ uint32_t prefill_tile(uint32_t hd, bool halves, int exact)
     return hd > 256 ? PCfg<512>::TILE : hd > 128 ? PCfg<256>::TILE : PCfg<128>::TILE;
 }
 
-hipError_t launch_xcopy(int kv, const DqArgs &a, hipStream_t s)
+hipError_t launch_xcopy(int kv, const XcopyArgs &a, hipStream_t s)
 {
     const uint64_t n = (uint64_t)a.n_kv * a.np * (a.hd / 8);
     if (n == 0 || a.hd % 8)
