@@ -453,8 +453,8 @@ int run_split(janas_attn *a, int kv, int gate_mode, const janas_attn_seq *seqs,
             int rc = describe(a, kv, seqs[s0 + i], d);
             if (rc)
                 return rc;
-            d.wg0 = wg;
-            d.mg0 = mg;
+            d.wg0 = args.wg0s[i] = wg;
+            d.mg0 = args.mg0s[i] = mg;
             d.part0 = rows;
             d.rtiles = (d.rtiles + args.mt - 1) / args.mt;
             args.once &= d.rtiles == 1;
@@ -839,8 +839,8 @@ int run_prefill_launch(janas_attn *a, int kv, int gate_mode,
                     return rc;
                 if ((!exact && prefill_halves(a, kv, d)) != (hv == 1))
                     continue;
-                d.wg0 = wg;
-                d.mg0 = mg;
+                d.wg0 = args.wg0s[m] = wg;
+                d.mg0 = args.mg0s[m] = mg;
                 d.nseg = prefill_segments(a, d, hv == 1, exact);
                 d.part0 = 0;
                 uint64_t nwg = (uint64_t)a->n_kv * d.nseg *

@@ -77,6 +77,8 @@ struct SplitArgs {
        8, 16, 32 below the row's largest score), [0] all rows, [1] rows past
        16384 positions - or null when off */
     unsigned long long *skip;
+    /* seq[i].wg0 and seq[i].mg0 again, side by side (seq_index) */
+    uint32_t wg0s[kMaxSeqs], mg0s[kMaxSeqs];
 };
 
 /* The causal MFMA pass over whole prompts (prefill, chunked prefill). */
@@ -100,6 +102,8 @@ struct PrefillArgs {
                               (prefill_exact_kernel): the planes of the copy
                               the sequences' k and v point at (1 int8, 2
                               int16; launch_xcopy), scales from ks / vs */
+    /* seq[i].wg0 and seq[i].mg0 again, side by side (seq_index) */
+    uint32_t wg0s[kMaxSeqs], mg0s[kMaxSeqs];
 };
 
 /* An int8 / int16 cache's rows of positions p0 .. p0 + np - 1 as the
@@ -148,21 +152,32 @@ struct Q8kArgs {
 };
 
 /* Launchers (attn_split.hip). Return hipSuccess or the launch's error. */
+/* The argument a workgroup's id is made from (n_any: the workgroup count,
+   or the KV head count), the sequence count and the sequences' starts in
+   scalar registers at a kernel's first instruction: asked for together,
+   they come in one round trip (left to the scheduler, the starts went out
+   only after the wait for the id's argument) */
+__device__ __forceinline__ void starts_early(uint32_t n_any, uint32_t n_seqs,
+                                             const uint32_t *starts)
+{
+    static_assert(kMaxSeqs == 16, "the starts as 15 scalar operands");
+    asm volatile("" ::"s"(n_any), "s"(n_seqs), "s"(starts[1]), "s"(starts[2]), "s"(starts[3]),
+                 "s"(starts[4]), "s"(starts[5]), "s"(starts[6]), "s"(starts[7]),
+                 "s"(starts[8]), "s"(starts[9]), "s"(starts[10]), "s"(starts[11]),
+                 "s"(starts[12]), "s"(starts[13]), "s"(starts[14]), "s"(starts[15]));
+}
 /* The sequence of a launch that workgroup id belongs to: the last whose
-   first workgroup (start, wg0 or mg0) is at or below id. With several
-   sequences every start is read at once - independent argument loads
-   rather than a chain of one round trip a sequence; a launch of one reads
-   none. */
-template <class Args>
-__device__ __forceinline__ uint32_t seq_index(const Args &A, uint32_t SeqDesc::*start,
+   first workgroup (starts[i]: the launch's wg0s or mg0s, the sequences'
+   wg0 or mg0 side by side) is at or below id. Branch-free, so the 64 bytes
+   of starts are read with the sequence count, in the arguments' first
+   round trip, and the sequence's own descriptor in the second. */
+__device__ __forceinline__ uint32_t seq_index(const uint32_t *starts, uint32_t n_seqs,
                                               uint32_t id)
 {
     uint32_t si = 0;
-    if (A.n_seqs <= 1)
-        return 0;
 #pragma unroll
     for (uint32_t i = 1; i < kMaxSeqs; i++)
-        si += i < A.n_seqs && A.seq[i].*start <= id;
+        si += i < n_seqs && starts[i] <= id;
     return si;
 }
 

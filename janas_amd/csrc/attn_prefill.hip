@@ -256,9 +256,11 @@ __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
        blocks alike. With contiguous runs a XCD alone (16 / 2 / 256 at 8k:
        one KV head over 4 XCDs) took either the longest blocks or the
        shortest: 1345 against 895 us. */
+    if constexpr (!ONE)
+        starts_early(A.n_kv, A.n_seqs, A.wg0s);
     const uint32_t S = 8u >> min(__builtin_ctz(A.n_kv | 8u), 3);
     const uint32_t id = xcd_remap_striped(blockIdx.x, gridDim.x, S);
-    const uint32_t si = ONE ? 0 : seq_index(A, &SeqDesc::wg0, id);
+    const uint32_t si = ONE ? 0 : seq_index(A.wg0s, A.n_seqs, id);
     PBlock P;
     P.sq = &A.seq[si];
     const SeqDesc &sq = *P.sq;
@@ -1662,8 +1664,10 @@ constexpr uint32_t kPMergeBatch = 4;
 template <bool ONE>
 __global__ __launch_bounds__(kPMergeThreads) void pmerge_kernel(const PrefillArgs A)
 {
+    if constexpr (!ONE)
+        starts_early(A.n_wg, A.n_seqs, A.mg0s);
     const uint32_t id = blockIdx.x;
-    const uint32_t si = ONE ? 0 : seq_index(A, &SeqDesc::mg0, id);
+    const uint32_t si = ONE ? 0 : seq_index(A.mg0s, A.n_seqs, id);
     const SeqDesc &sq = A.seq[si];
     const uint32_t hd = A.hd, nseg = sq.nseg, c4 = hd / 4;
     const uint64_t pair = (uint64_t)(id - sq.mg0) * kPMergeThreads + threadIdx.x;

@@ -171,14 +171,20 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t g = lane >> 4, l16 = lane & 15;
+    if constexpr (!ONE)
+        starts_early(A.n_wg, A.n_seqs, A.wg0s);
     const uint32_t id = xcd_remap(blockIdx.x, A.n_wg);
     uint32_t si = 0;
     if constexpr (!ONE)
-        si = seq_index(A, &SeqDesc::wg0, id);
+        si = seq_index(A.wg0s, A.n_seqs, id);
     const SeqDesc &sq = A.seq[si];
     const uint32_t G = A.group, hd = A.hd;
-    /* the cache and query addresses with the first batch of argument loads */
-    asm volatile("" ::"s"(sq.k), "s"(sq.v), "s"(sq.q), "s"(A.n_head));
+    /* the descriptor fields the workgroup starts from (the cache and query
+       addresses among them) in one round trip: left to the scheduler,
+       a second batch of them went out after a wait for the first */
+    asm volatile("" ::"s"(sq.k), "s"(sq.v), "s"(sq.q), "s"(A.n_head), "s"(sq.n),
+                 "s"(sq.pos0), "s"(sq.end), "s"(sq.c0), "s"(sq.span), "s"(sq.rtiles),
+                 "s"(sq.wg0), "s"(sq.cap), "s"(sq.last));
     const uint32_t local = id - sq.wg0;
     const uint32_t rt = local % sq.rtiles;
     const uint32_t c = sq.c0 + (local / sq.rtiles) % sq.span;
@@ -794,11 +800,13 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     __shared__ float4 sAcc[kMergeGroups][NV][kMergeLanes];
     __shared__ float sOut[Q8K ? 256 : 1];
     __shared__ Q8kLds sQ;
+    if constexpr (!ONE)
+        starts_early(A.n_wg, A.n_seqs, A.mg0s);
     const uint32_t id = blockIdx.x, tid = threadIdx.x;
     const uint32_t g = tid / kMergeLanes, cl = tid % kMergeLanes;
     uint32_t si = 0;
     if constexpr (!ONE)
-        si = seq_index(A, &SeqDesc::mg0, id);
+        si = seq_index(A.mg0s, A.n_seqs, id);
     const SeqDesc &sq = A.seq[si];
     const uint32_t hd = A.hd, G = A.group;
     const uint32_t local = id - sq.mg0;

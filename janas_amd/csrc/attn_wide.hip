@@ -117,14 +117,20 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t g16 = lane >> 4, l16 = lane & 15;
+    if constexpr (!ONE)
+        starts_early(A.n_wg, A.n_seqs, A.wg0s);
     const uint32_t id = xcd_remap(blockIdx.x, A.n_wg);
     uint32_t si = 0;
     if constexpr (!ONE)
-        si = seq_index(A, &SeqDesc::wg0, id);
+        si = seq_index(A.wg0s, A.n_seqs, id);
     const SeqDesc &sq = A.seq[si];
     const uint32_t G = A.group, hd = A.hd;
-    /* the cache and query addresses with the first batch of argument loads */
-    asm volatile("" ::"s"(sq.k), "s"(sq.v), "s"(sq.q), "s"(A.n_head));
+    /* the descriptor fields the workgroup starts from (the cache and query
+       addresses among them) in one round trip: left to the scheduler,
+       a second batch of them went out after a wait for the first */
+    asm volatile("" ::"s"(sq.k), "s"(sq.v), "s"(sq.q), "s"(A.n_head), "s"(sq.n),
+                 "s"(sq.pos0), "s"(sq.end), "s"(sq.c0), "s"(sq.span), "s"(sq.rtiles),
+                 "s"(sq.wg0), "s"(sq.cap), "s"(sq.last));
     const uint32_t local = id - sq.wg0;
     const uint32_t rt = local % sq.rtiles;
     const uint32_t c = sq.c0 + (local / sq.rtiles) % sq.span;
