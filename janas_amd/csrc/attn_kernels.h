@@ -152,19 +152,20 @@ struct Q8kArgs {
 };
 
 /* Launchers (attn_split.hip). Return hipSuccess or the launch's error. */
-/* The argument a workgroup's id is made from (n_any: the workgroup count,
-   or the KV head count), the sequence count and the sequences' starts in
+/* The arguments a workgroup's id is made from (a, b: the workgroup count,
+   the KV head count), the sequence count and the sequences' starts in
    scalar registers at a kernel's first instruction: asked for together,
    they come in one round trip (left to the scheduler, the starts went out
-   only after the wait for the id's argument) */
-__device__ __forceinline__ void starts_early(uint32_t n_any, uint32_t n_seqs,
+   only after the wait for the id's arguments) */
+__device__ __forceinline__ void starts_early(uint32_t a, uint32_t b, uint32_t n_seqs,
                                              const uint32_t *starts)
 {
     static_assert(kMaxSeqs == 16, "the starts as 15 scalar operands");
-    asm volatile("" ::"s"(n_any), "s"(n_seqs), "s"(starts[1]), "s"(starts[2]), "s"(starts[3]),
-                 "s"(starts[4]), "s"(starts[5]), "s"(starts[6]), "s"(starts[7]),
-                 "s"(starts[8]), "s"(starts[9]), "s"(starts[10]), "s"(starts[11]),
-                 "s"(starts[12]), "s"(starts[13]), "s"(starts[14]), "s"(starts[15]));
+    asm volatile("" ::"s"(a), "s"(b), "s"(n_seqs), "s"(starts[1]), "s"(starts[2]),
+                 "s"(starts[3]), "s"(starts[4]), "s"(starts[5]), "s"(starts[6]),
+                 "s"(starts[7]), "s"(starts[8]), "s"(starts[9]), "s"(starts[10]),
+                 "s"(starts[11]), "s"(starts[12]), "s"(starts[13]), "s"(starts[14]),
+                 "s"(starts[15]));
 }
 /* The sequence of a launch that workgroup id belongs to: the last whose
    first workgroup (starts[i]: the launch's wg0s or mg0s, the sequences'

@@ -257,13 +257,19 @@ __device__ __forceinline__ PBlock block_of(const PrefillArgs &A)
        one KV head over 4 XCDs) took either the longest blocks or the
        shortest: 1345 against 895 us. */
     if constexpr (!ONE)
-        starts_early(A.n_kv, A.n_seqs, A.wg0s);
+        starts_early(A.n_wg, A.n_kv, A.n_seqs, A.wg0s);
     const uint32_t S = 8u >> min(__builtin_ctz(A.n_kv | 8u), 3);
-    const uint32_t id = xcd_remap_striped(blockIdx.x, gridDim.x, S);
+    /* the launch's grid is n_wg workgroups (read with the other arguments:
+       the grid size is an implicit argument past them, in a cache line of
+       its own) */
+    const uint32_t id = xcd_remap_striped(blockIdx.x, A.n_wg, S);
     const uint32_t si = ONE ? 0 : seq_index(A.wg0s, A.n_seqs, id);
     PBlock P;
     P.sq = &A.seq[si];
     const SeqDesc &sq = *P.sq;
+    /* the descriptor fields the block starts from in one round trip */
+    asm volatile("" ::"s"(sq.n), "s"(sq.nseg), "s"(sq.wg0), "s"(sq.pos0), "s"(sq.end),
+                 "s"(sq.cap), "s"(sq.last), "s"(sq.q), "s"(sq.k), "s"(sq.v));
     const uint32_t G = A.group;
     const uint32_t R = sq.n * G;
     const uint32_t nrb = (R + kPBlock - 1) / kPBlock;
@@ -1665,7 +1671,7 @@ template <bool ONE>
 __global__ __launch_bounds__(kPMergeThreads) void pmerge_kernel(const PrefillArgs A)
 {
     if constexpr (!ONE)
-        starts_early(A.n_wg, A.n_seqs, A.mg0s);
+        starts_early(A.n_wg, A.n_wg, A.n_seqs, A.mg0s);
     const uint32_t id = blockIdx.x;
     const uint32_t si = ONE ? 0 : seq_index(A.mg0s, A.n_seqs, id);
     const SeqDesc &sq = A.seq[si];

@@ -172,7 +172,7 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t g = lane >> 4, l16 = lane & 15;
     if constexpr (!ONE)
-        starts_early(A.n_wg, A.n_seqs, A.wg0s);
+        starts_early(A.n_wg, A.n_wg, A.n_seqs, A.wg0s);
     const uint32_t id = xcd_remap(blockIdx.x, A.n_wg);
     uint32_t si = 0;
     if constexpr (!ONE)
@@ -801,7 +801,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
     __shared__ float sOut[Q8K ? 256 : 1];
     __shared__ Q8kLds sQ;
     if constexpr (!ONE)
-        starts_early(A.n_wg, A.n_seqs, A.mg0s);
+        starts_early(A.n_wg, A.n_wg, A.n_seqs, A.mg0s);
     const uint32_t id = blockIdx.x, tid = threadIdx.x;
     const uint32_t g = tid / kMergeLanes, cl = tid % kMergeLanes;
     uint32_t si = 0;

@@ -118,7 +118,7 @@ __global__ __launch_bounds__(256) void wide_kernel(const SplitArgs A)
     const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint32_t g16 = lane >> 4, l16 = lane & 15;
     if constexpr (!ONE)
-        starts_early(A.n_wg, A.n_seqs, A.wg0s);
+        starts_early(A.n_wg, A.n_wg, A.n_seqs, A.wg0s);
     const uint32_t id = xcd_remap(blockIdx.x, A.n_wg);
     uint32_t si = 0;
     if constexpr (!ONE)
