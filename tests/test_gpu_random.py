@@ -24,7 +24,7 @@ from oracle import orc
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 24
+N_CASES = 48
 CHUNK = 256
 
 
@@ -188,7 +188,7 @@ def draw_exact(i):
                 seed=9600 + 10 * i)
 
 
-@pytest.mark.parametrize("i", range(16))
+@pytest.mark.parametrize("i", range(32))
 def test_random_exact_prefill(gpu, i):
     """The exact kernel on seeded random geometries, two sequences a launch
     (the second a shorter, later call over the same cache, so their copies
