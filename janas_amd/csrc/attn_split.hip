@@ -603,6 +603,11 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
     }
     if constexpr (!Q16) {
         const float up = ldexpf(1.0f, pe);
+        /* the lane's weight plane, hi = f16(pv) on even lanes and lo =
+           f16(pv - hi) on odd ones, as one multiply-add rounded once to f16:
+           pv - 0 hi is pv, and pv - hi is exact in f32, so these are
+           split_hl's planes, without its second conversion and the select */
+        const float oddf = (l16 & 1) ? 1.0f : 0.0f;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const float mm = m[mt] == -INFINITY ? 0.0f : m[mt];
@@ -611,15 +616,22 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
             for (int s = 0; s < kSNG; s++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
+                    /* the reference's cutoff (a weight below e^-80 is 0,
+                       attention.c:580) needs no test here: such a weight is
+                       below 2^-115, its planes below are f16 zeros (pv is
+                       below 2^-102), and it cannot change a sum that holds
+                       the wave's largest weight, 1 (a masked score gives
+                       exp2(-inf) = 0) */
                     const float d = sv[mt][s][i] - mm;
-                    const float pw = d >= kCut2 ? __builtin_amdgcn_exp2f(d) : 0.0f;
+                    const float pw = __builtin_amdgcn_exp2f(d);
                     lsum += pw;
                     float pv = pw * up;
                     if constexpr (S::SCALED)
                         pv *= vz[s][i];
-                    _Float16 hi, lo;
-                    split_hl(pv, hi, lo);
-                    pa[mt][s][i] = (l16 & 1) ? lo : hi;
+                    /* pv as rounded (no product fused into the conversion) */
+                    asm volatile("" : "+v"(pv));
+                    const _Float16 hi = (_Float16)pv;
+                    pa[mt][s][i] = (_Float16)__builtin_fmaf(-oddf, (float)hi, pv);
                 }
             lsum = sum_x32(sum_x16(lsum));
             if (lane < 16 && !(lane & 1)) {
