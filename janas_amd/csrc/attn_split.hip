@@ -478,6 +478,30 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
         /* the key scales of the lane's 4 positions, one read for all of
            them (read under the mask below, each was a branch and a wait of
            its own) */
+        if constexpr (Q16) {
+            /* INT16: lane l16 & 1 = b makes the scores of positions 2 b and
+               2 b + 1 of its four, its neighbour (the row's other plane) the
+               other two: from its own plane's sum and the neighbour's, in
+               natural units, the reference's score bit for bit. So each
+               score, weight and quantized weight is made once, not in both
+               lanes of a row */
+            const uint32_t b = l16 & 1;
+            const float2 kz2 = *(const float2 *)&sKs[w][kSG * s + 4 * g + 2 * b];
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const float own = b ? sa[mt][2 + j] : sa[mt][j];
+                    const float nbr = from_x1(b ? sa[mt][j] : sa[mt][2 + j]);
+                    float x = q16_score(b ? nbr : own, b ? own : nbr, qsc[mt], A.scale,
+                                        j ? kz2.y : kz2.x);
+                    const uint32_t p = p0w + kSG * s + 4 * g + 2 * b + j;
+                    const bool vis = (p >= rlo[mt]) & (p <= rhi[mt]);
+                    sv[mt][s][j] = vis ? x : -INFINITY;
+                    m[mt] = fmaxf(m[mt], sv[mt][s][j]);
+                }
+            continue;
+        }
         f4 kz = f4{1.0f, 1.0f, 1.0f, 1.0f};
         if constexpr (S::SCALED)
             kz = *(const f4 *)&sKs[w][kSG * s + 4 * g];
@@ -486,18 +510,9 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t pl = kSG * s + 4 * g + i, p = p0w + pl;
-            float x;
-            if constexpr (Q16) {
-                /* natural units, the reference's score bit for bit */
-                const float other = from_x1(sa[mt][i]);
-                const bool odd = l16 & 1;
-                x = q16_score(odd ? other : sa[mt][i], odd ? sa[mt][i] : other, qsc[mt], A.scale,
-                              kz[i]);
-            } else {
-                x = (sa[mt][i] + from_x1(sa[mt][i])) * qs2[mt];
-                if constexpr (S::SCALED)
-                    x *= kz[i];
-            }
+            float x = (sa[mt][i] + from_x1(sa[mt][i])) * qs2[mt];
+            if constexpr (S::SCALED)
+                x *= kz[i];
             if constexpr (MT == 1) {
                 sv[mt][s][i] = p >= rlo[mt] && p <= rhi[mt] ? x : -INFINITY;
                 m[mt] = fmaxf(m[mt], sv[mt][s][i]);
@@ -528,13 +543,16 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
         }
     }
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
+    for (int mt = 0; mt < MT; mt++) {
+        if constexpr (Q16)
+            m[mt] = fmaxf(m[mt], from_x1(m[mt]));   /* the row's two lanes */
         m[mt] = max_x32(max_x16(m[mt]));
+    }
     /* the value scales of the lane's 16 positions, in registers */
     f4 vz[kSNG];
 #pragma unroll
     for (int s = 0; s < kSNG; s++)
-        vz[s] = S::SCALED ? *(const f4 *)&sVs[w][kSG * s + 4 * g] : f4{1.0f, 1.0f, 1.0f, 1.0f};
+        vz[s] = S::SCALED && !Q16 ? *(const f4 *)&sVs[w][kSG * s + 4 * g] : f4{1.0f, 1.0f, 1.0f, 1.0f};
     h4 pa[MT][kSNG];
     if constexpr (Q16) {
         /* INT16: the chunk's largest score over the 4 waves, the weights
@@ -547,7 +565,13 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
             for (int mt = 0; mt < MT; mt++)
                 sM[w][kTileRows * mt + (lane >> 1)] = m[mt];
         __syncthreads();
-        float pv[MT][kSNG][4];
+        /* the lane's two positions of each group (2 b, 2 b + 1) */
+        const uint32_t b = l16 & 1;
+        float2 vz2[kSNG];
+#pragma unroll
+        for (int s = 0; s < kSNG; s++)
+            vz2[s] = *(const float2 *)&sVs[w][kSG * s + 4 * g + 2 * b];
+        float pv[MT][kSNG][2];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const uint32_t rr = kTileRows * mt + qr;
@@ -557,14 +581,14 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
 #pragma unroll
             for (int s = 0; s < kSNG; s++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float wt = det_weight(sv[mt][s][i], mm);
+                for (int j = 0; j < 2; j++) {
+                    const float wt = det_weight(sv[mt][s][j], mm);
                     lsum += wt;
-                    pv[mt][s][i] = wt * vz[s][i];
-                    vmx = fmaxf(vmx, pv[mt][s][i]);
+                    pv[mt][s][j] = wt * (j ? vz2[s].y : vz2[s].x);
+                    vmx = fmaxf(vmx, pv[mt][s][j]);
                 }
-            vmx = max_x32(max_x16(vmx));
-            lsum = sum_x32(sum_x16(lsum));
+            vmx = max_x32(max_x16(fmaxf(vmx, from_x1(vmx))));
+            lsum = sum_x32(sum_x16(lsum + from_x1(lsum)));
             if (lane < 16 && !(lane & 1)) {
                 sX[w][kTileRows * mt + (lane >> 1)] = vmx;
                 sL[w][kTileRows * mt + (lane >> 1)] = lsum;
@@ -575,12 +599,17 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
         for (int mt = 0; mt < MT; mt++) {
             const uint32_t rr = kTileRows * mt + qr;
             const float inv = q16_inv(fmaxf(fmaxf(sX[0][rr], sX[1][rr]), fmaxf(sX[2][rr], sX[3][rr])));
+            /* the lane's plane (b = 0: w >> 8, 1: w & 255) of all four
+               positions: its own two quantized weights and its neighbour's */
+            const uint32_t sh = b ? 0 : 8;
 #pragma unroll
             for (int s = 0; s < kSNG; s++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int32_t q = q16_round(pv[mt][s][i], inv);
-                    pa[mt][s][i] = (l16 & 1) ? (_Float16)(q & 255) : (_Float16)(q >> 8);
+                for (int j = 0; j < 2; j++) {
+                    const uint32_t q = (uint32_t)q16_round(pv[mt][s][j], inv);
+                    const uint32_t r = __builtin_amdgcn_update_dpp(0u, q, 0xB1, 0xf, 0xf, false);
+                    pa[mt][s][j] = (_Float16)(float)(((b ? r : q) >> sh) & 255);
+                    pa[mt][s][2 + j] = (_Float16)(float)(((b ? q : r) >> sh) & 255);
                 }
         }
     }
