@@ -28,6 +28,21 @@ def _cache_dir(tmp_path_factory):
         os.environ["XDG_CACHE_HOME"] = old
 
 
+@pytest.fixture(scope="session", autouse=True)
+def _float_unless_named():
+    """Instances a test makes without naming a way compute FLOAT. AUTO's way
+    is a measurement of both ways' speed on the device at the first call
+    (the reference's rule, attention.c:1183-1247); where the two run within
+    the measurement's noise of each other it can fall either way, and a test
+    that compares with the FLOAT restatement, or a block with its tokens,
+    needs one way. The tests of AUTO name it."""
+    from janas_amd import attention as att
+    defaults = att.Attention.__init__.__defaults__
+    att.Attention.__init__.__defaults__ = (defaults[0], att.FLOAT)
+    yield
+    att.Attention.__init__.__defaults__ = defaults
+
+
 @pytest.fixture(scope="session")
 def gpu():
     """The GPU tests run where a GPU is: fail, never skip, without one."""

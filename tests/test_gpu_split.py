@@ -260,7 +260,7 @@ def normal_cache(seed, count):
 
 
 def run_block(c, kv, gpu, pos0, window=0, last=None, per_token=False,
-              scores=janas_amd.AUTO):
+              scores=janas_amd.FLOAT):
     d = dict(k=to_dev(c["k"], gpu), v=to_dev(c["v"], gpu),
              q=to_dev(c["q"], gpu), cap=c["L"], n=c["n"], pos0=pos0)
     if c["ks"] is not None:
