@@ -414,16 +414,13 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
        positions 16 s + 4 g + i), each K operand read once for the MT
        tiles ---- */
     const uint32_t p0w = t0 + w * kSWP;
-    /* two row tiles (a block of tokens, a verify): whether every row of
-       the tiles that exists sees all 64 positions of the wave (a chunk
-       inside every row's range), so that its scores take no mask. A row
-       past R is left out; its numbers are never stored. The test is the
-       same for the whole wave (a vote), so the branch below is a scalar
-       one. A 64-token block at 4096 positions 44.0-44.9 -> 42.8-43.9 us;
-       a decode (one tile) was no faster, its int8 instance slower, and
-       keeps the mask under each score */
+    /* whether every row of the tiles that exists sees all 64 positions of
+       the wave (a chunk inside every row's range), so that its scores take
+       no mask. A row past R is left out; its numbers are never stored. The
+       test is the same for the whole wave (a vote), so the branch below is
+       a scalar one */
     bool full = false;
-    if constexpr (MT > 1) {
+    {
         bool seen = true;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
@@ -502,57 +499,54 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
                 }
             continue;
         }
-        f4 kz = f4{1.0f, 1.0f, 1.0f, 1.0f};
+        /* FLOAT: the same split of a row's four positions between its two
+           lanes; a score is (high plane's sum + low plane's) x scale, the
+           same in both lanes */
+        const uint32_t b = l16 & 1;
+        float2 kz2 = make_float2(1.0f, 1.0f);
         if constexpr (S::SCALED)
-            kz = *(const f4 *)&sKs[w][kSG * s + 4 * g];
+            kz2 = *(const float2 *)&sKs[w][kSG * s + 4 * g + 2 * b];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t pl = kSG * s + 4 * g + i, p = p0w + pl;
-            float x = (sa[mt][i] + from_x1(sa[mt][i])) * qs2[mt];
-            if constexpr (S::SCALED)
-                x *= kz[i];
-            if constexpr (MT == 1) {
-                sv[mt][s][i] = p >= rlo[mt] && p <= rhi[mt] ? x : -INFINITY;
-                m[mt] = fmaxf(m[mt], sv[mt][s][i]);
-            } else {
-                sv[mt][s][i] = x;
+            for (int j = 0; j < 2; j++) {
+                const float y0 = sa[mt][j] + from_x1(sa[mt][j]);
+                const float y1 = sa[mt][2 + j] + from_x1(sa[mt][2 + j]);
+                float x = (b ? y1 : y0) * qs2[mt];
+                if constexpr (S::SCALED)
+                    x *= j ? kz2.y : kz2.x;
+                sv[mt][s][j] = x;
             }
+        /* both bounds tested, then one select: no part of the score under a
+           branch of its own; with two row tiles only where a row does not
+           see all of the wave's positions */
+        if (!full) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const uint32_t p = p0w + kSG * s + 4 * g + 2 * b + j;
+                    const bool vis = (p >= rlo[mt]) & (p <= rhi[mt]);
+                    sv[mt][s][j] = vis ? sv[mt][s][j] : -INFINITY;
+                }
         }
-        if constexpr (MT > 1) {
-            if (full) {
 #pragma unroll
-                for (int mt = 0; mt < MT; mt++)
+        for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        m[mt] = fmaxf(m[mt], sv[mt][s][i]);
-            } else {
-                /* both bounds tested, then one select: no part of the
-                   score under a branch of its own */
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const uint32_t p = p0w + kSG * s + 4 * g + i;
-                        const bool vis = (p >= rlo[mt]) & (p <= rhi[mt]);
-                        sv[mt][s][i] = vis ? sv[mt][s][i] : -INFINITY;
-                        m[mt] = fmaxf(m[mt], sv[mt][s][i]);
-                    }
-            }
-        }
+            for (int j = 0; j < 2; j++)
+                m[mt] = fmaxf(m[mt], sv[mt][s][j]);
     }
+    /* over the row's two lanes, then its 4 lane groups */
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        if constexpr (Q16)
-            m[mt] = fmaxf(m[mt], from_x1(m[mt]));   /* the row's two lanes */
-        m[mt] = max_x32(max_x16(m[mt]));
-    }
-    /* the value scales of the lane's 16 positions, in registers */
-    f4 vz[kSNG];
+    for (int mt = 0; mt < MT; mt++)
+        m[mt] = max_x32(max_x16(fmaxf(m[mt], from_x1(m[mt]))));
+    /* the lane's two positions of each group (2 b, 2 b + 1) and their value
+       scales, in registers */
+    const uint32_t b = l16 & 1;
+    float2 vz2[kSNG];
 #pragma unroll
     for (int s = 0; s < kSNG; s++)
-        vz[s] = S::SCALED && !Q16 ? *(const f4 *)&sVs[w][kSG * s + 4 * g] : f4{1.0f, 1.0f, 1.0f, 1.0f};
+        vz2[s] = S::SCALED ? *(const float2 *)&sVs[w][kSG * s + 4 * g + 2 * b] : make_float2(1.0f, 1.0f);
     h4 pa[MT][kSNG];
     if constexpr (Q16) {
         /* INT16: the chunk's largest score over the 4 waves, the weights
@@ -565,12 +559,6 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
             for (int mt = 0; mt < MT; mt++)
                 sM[w][kTileRows * mt + (lane >> 1)] = m[mt];
         __syncthreads();
-        /* the lane's two positions of each group (2 b, 2 b + 1) */
-        const uint32_t b = l16 & 1;
-        float2 vz2[kSNG];
-#pragma unroll
-        for (int s = 0; s < kSNG; s++)
-            vz2[s] = *(const float2 *)&sVs[w][kSG * s + 4 * g + 2 * b];
         float pv[MT][kSNG][2];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
@@ -621,10 +609,8 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
         float vm = 0.0f;
 #pragma unroll
         for (int s = 0; s < kSNG; s++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                vm = fmaxf(vm, vz[s][i]);
-        vm = max_x32(max_x16(vm));
+            vm = fmaxf(vm, fmaxf(vz2[s].x, vz2[s].y));
+        vm = max_x32(max_x16(fmaxf(vm, from_x1(vm))));
         int ev = 0;
         if (vm > 0.0f && vm < INFINITY)
             frexpf(vm, &ev);
@@ -632,37 +618,45 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
     }
     if constexpr (!Q16) {
         const float up = ldexpf(1.0f, pe);
-        /* the lane's weight plane, hi = f16(pv) on even lanes and lo =
-           f16(pv - hi) on odd ones, as one multiply-add rounded once to f16:
-           pv - 0 hi is pv, and pv - hi is exact in f32, so these are
-           split_hl's planes, without its second conversion and the select */
-        const float oddf = (l16 & 1) ? 1.0f : 0.0f;
+        /* a lane makes both f16 planes of its own two weights, hi = f16(pv)
+           and lo = f16(pv - hi), each as one multiply-add rounded once to
+           f16 (pv - 0 hi is pv, and pv - hi is exact in f32: split_hl's
+           planes); it keeps its row plane's (b = 0: hi, 1: lo) and swaps the
+           other for its neighbour's, so it holds its plane of all four */
+        const float keepf = b ? -1.0f : -0.0f, sendf = b ? 0.0f : -1.0f;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const float mm = m[mt] == -INFINITY ? 0.0f : m[mt];
             float lsum = 0.0f;
 #pragma unroll
-            for (int s = 0; s < kSNG; s++)
+            for (int s = 0; s < kSNG; s++) {
+                h2 keep, send;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
+                for (int j = 0; j < 2; j++) {
                     /* the reference's cutoff (a weight below e^-80 is 0,
                        attention.c:580) needs no test here: such a weight is
-                       below 2^-115, its planes below are f16 zeros (pv is
-                       below 2^-102), and it cannot change a sum that holds
-                       the wave's largest weight, 1 (a masked score gives
+                       below 2^-115, its planes are f16 zeros (pv is below
+                       2^-102), and it cannot change a sum that holds the
+                       wave's largest weight, 1 (a masked score gives
                        exp2(-inf) = 0) */
-                    const float d = sv[mt][s][i] - mm;
+                    const float d = sv[mt][s][j] - mm;
                     const float pw = __builtin_amdgcn_exp2f(d);
                     lsum += pw;
                     float pv = pw * up;
                     if constexpr (S::SCALED)
-                        pv *= vz[s][i];
+                        pv *= j ? vz2[s].y : vz2[s].x;
                     /* pv as rounded (no product fused into the conversion) */
                     asm volatile("" : "+v"(pv));
-                    const _Float16 hi = (_Float16)pv;
-                    pa[mt][s][i] = (_Float16)__builtin_fmaf(-oddf, (float)hi, pv);
+                    const float hi = (float)(_Float16)pv;
+                    keep[j] = (_Float16)__builtin_fmaf(keepf, hi, pv);
+                    send[j] = (_Float16)__builtin_fmaf(sendf, hi, pv);
                 }
-            lsum = sum_x32(sum_x16(lsum));
+                const uint32_t kept = __builtin_bit_cast(uint32_t, keep);
+                const uint32_t got = __builtin_amdgcn_update_dpp(
+                    0u, __builtin_bit_cast(uint32_t, send), 0xB1, 0xf, 0xf, false);
+                pa[mt][s] = __builtin_bit_cast(h4, make_uint2(b ? got : kept, b ? kept : got));
+            }
+            lsum = sum_x32(sum_x16(lsum + from_x1(lsum)));
             if (lane < 16 && !(lane & 1)) {
                 sM[w][kTileRows * mt + (lane >> 1)] = m[mt];
                 sL[w][kTileRows * mt + (lane >> 1)] = lsum;
