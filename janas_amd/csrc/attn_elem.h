@@ -259,12 +259,16 @@ __device__ __forceinline__ float exp_det(float x)
    scale, the score scale and the key scale (attention_scores.h:73-81). The
    high sum times 256 may pass 2^31 on its own: unsigned, it wraps back
    into the int32 sum, which the reference's bound keeps below 2^31 */
+__device__ __forceinline__ float q16_scale(int32_t s, float qsc, float scale, float ks)
+{
+#pragma clang fp contract(off)
+    return (float)s * qsc * scale * ks;
+}
 __device__ __forceinline__ float q16_score(float hi, float lo, float qsc, float scale,
                                            float ks)
 {
-#pragma clang fp contract(off)
     const int32_t s = (int32_t)((uint32_t)(int32_t)hi * 256u + (uint32_t)(int32_t)lo);
-    return (float)s * qsc * scale * ks;
+    return q16_scale(s, qsc, scale, ks);
 }
 
 /* a weight (att_weights_ref, attention.c:574-588): 0 below e^-80 of the

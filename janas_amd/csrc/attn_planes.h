@@ -21,6 +21,7 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef int i4 __attribute__((ext_vector_type(4)));   /* 16 bytes as int8 operands */
 
 /* 4 signed bytes (a word, the first in the low byte) to 4 halves, exactly:
    b ^ 0x80 = b + 128 under 0x64 is the half 1152 + b, less 1152 is b - one

@@ -161,6 +161,14 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
     constexpr int CR = S::REG > 32 * D * MT ? S::REG : 32 * D * MT;
     __shared__ __attribute__((aligned(1024))) char sR[kSW * CR];
     __shared__ __attribute__((aligned(16))) _Float16 sQ[2 * TR][D + 8];
+    /* INT16 over int8 keys, head sizes from 128: the scores are integer
+       products (v_mfma_i32_16x16x64_i8) of the keys as they are in memory
+       and the query's planes as bytes, x >> 8 and (x & 255) - 128; the
+       second plane's offset is given back as 128 times the key's sum, a
+       product of the keys with ones. The keys skip the widening to f16 */
+    constexpr bool RAWK = Q16 && D >= 128;
+    constexpr int KS8 = D / 64;   /* integer k-steps */
+    __shared__ __attribute__((aligned(16))) int8_t sQ8[RAWK ? 2 * TR : 1][RAWK ? D + 16 : 16];
     __shared__ float sQs[TR];
     __shared__ __attribute__((aligned(16))) float sM[kSW][TR];
     __shared__ __attribute__((aligned(16))) float sL[kSW][TR];
@@ -333,8 +341,13 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int32_t qi = ok && qcol[h] < hd ? q16_round(x[e], inv) : 0;
-                    sQ[2 * tr][qcol[h] + e] = (_Float16)(qi >> 8);
-                    sQ[2 * tr + 1][qcol[h] + e] = (_Float16)(qi & 255);
+                    if constexpr (RAWK) {
+                        sQ8[2 * tr][qcol[h] + e] = (int8_t)(qi >> 8);
+                        sQ8[2 * tr + 1][qcol[h] + e] = (int8_t)((qi & 255) - 128);
+                    } else {
+                        sQ[2 * tr][qcol[h] + e] = (_Float16)(qi >> 8);
+                        sQ[2 * tr + 1][qcol[h] + e] = (_Float16)(qi & 255);
+                    }
                 }
                 if (qcol[h] == 0)
                     sQs[tr] = mx / 32767.0f;
@@ -372,12 +385,19 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
     }
     __syncthreads();
     h8 qb[MT][KS];
+    i4 qb8[MT][KS8];
     float qs2[MT], qsc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
+        if constexpr (RAWK) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++)
-            qb[mt][ks] = *(const h8 *)&sQ[16 * mt + l16][32 * ks + 8 * g];
+            for (int ks = 0; ks < KS8; ks++)
+                qb8[mt][ks] = *(const i4 *)&sQ8[16 * mt + l16][64 * ks + 16 * g];
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+                qb[mt][ks] = *(const h8 *)&sQ[16 * mt + l16][32 * ks + 8 * g];
+        }
         qsc[mt] = sQs[kTileRows * mt + qr];
         qs2[mt] = qsc[mt] * A.scale * kLog2e;
     }
@@ -408,6 +428,14 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
             *(h4 *)(rb + 16 * slot<D>(u, row) + 8 * half) = hi;
             *(h4 *)(rb + S::PLB + 16 * slot<D>(u, row) + 8 * half) = lo;
         }
+    };
+
+    /* a K group's 16 B as they are (RAWK): rows of D bytes, D / 16 units
+       swizzled as an f16 row of D / 2 numbers */
+    auto stage_raw = [&](const u4 &x0, int l) {
+        const uint32_t row = off[l] >> 16;
+        const uint32_t cb = (1024 * l + 16 * lane) % S::MRB;
+        *(u4 *)(myR + row * D + 16 * slot<D / 2>(cb / 16, row)) = x0;
     };
 
     /* ---- scores, a group at a time as its K lands (lane: MFMA row l16 at
@@ -446,10 +474,52 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
             if (s > 0)
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-            for (int l = 0; l < LG; l++)
-                stage(t[l], l);
+            for (int l = 0; l < LG; l++) {
+                if constexpr (RAWK)
+                    stage_raw(t[l], l);
+                else
+                    stage(t[l], l);
+            }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if constexpr (RAWK) {
+            /* INT16 on the integer matrix cores: the planes' sums and the
+               keys' sums, then the same exact score as below */
+            i4 si[MT], sk = i4{0, 0, 0, 0};
+            const i4 ones = i4{0x01010101, 0x01010101, 0x01010101, 0x01010101};
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+                si[mt] = i4{0, 0, 0, 0};
+#pragma unroll
+            for (int ks = 0; ks < KS8; ks++) {
+                const i4 ka = *(const i4 *)(myR + l16 * D + 16 * slot<D / 2>(4 * ks + g, l16));
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    si[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka, qb8[mt][ks], si[mt], 0, 0, 0);
+                sk = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka, ones, sk, 0, 0, 0);
+            }
+            const uint32_t b = l16 & 1;
+            const float2 kz2 = *(const float2 *)&sKs[w][kSG * s + 4 * g + 2 * b];
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const uint32_t own = (uint32_t)(b ? si[mt][2 + j] : si[mt][j]);
+                    const uint32_t nbr = __builtin_amdgcn_update_dpp(
+                        0u, (uint32_t)(b ? si[mt][j] : si[mt][2 + j]), 0xB1, 0xf, 0xf, false);
+                    const uint32_t ks1 = (uint32_t)(b ? sk[2 + j] : sk[j]);
+                    /* 256 hi + (lo - 128) + 128 x the keys' sum, as unsigned
+                       words (the int32 sum wraps back into range) */
+                    const uint32_t hi = b ? nbr : own, lo = b ? own : nbr;
+                    float x = q16_scale((int32_t)(hi * 256u + lo + ks1 * 128u), qsc[mt],
+                                        A.scale, j ? kz2.y : kz2.x);
+                    const uint32_t p = p0w + kSG * s + 4 * g + 2 * b + j;
+                    const bool vis = (p >= rlo[mt]) & (p <= rhi[mt]);
+                    sv[mt][s][j] = vis ? x : -INFINITY;
+                    m[mt] = fmaxf(m[mt], sv[mt][s][j]);
+                }
+            continue;
+        }
         f4 sa[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
