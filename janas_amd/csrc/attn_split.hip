@@ -1015,6 +1015,11 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 #pragma unroll
     for (int u = 0; u < NV; u++)
         ag[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    /* the lane's addresses in chunk clo; a chunk's rows are R further on
+       (one multiply-add a load) */
+    const char *const ml0 = (const char *)((const float2 *)A.part_ml + base);
+    const char *const acc0 = (const char *)(A.part_acc + base * hd + (colok ? col : 0));
+    const uint32_t rml = R * 8, racc = R * hd * 4;   /* bytes a chunk */
     for (uint32_t i0 = g; i0 < nc; i0 += kMergeGroups * NB) {
         float2 ml[NB];
         float4 v[NB][NV];
@@ -1022,9 +1027,8 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             const uint32_t i = i0 + kMergeGroups * b < nc ? i0 + kMergeGroups * b : nc - 1;
-            const uint64_t pr = base + (uint64_t)i * R;
-            ml[b] = *(const float2 *)(A.part_ml + pr * 2);
-            const float *src = A.part_acc + pr * hd + (colok ? col : 0);
+            ml[b] = *(const float2 *)(ml0 + (uint64_t)i * rml);
+            const float *src = (const float *)(acc0 + (uint64_t)i * racc);
             if constexpr (CPL >= 4) {
 #pragma unroll
                 for (int u = 0; u < NV; u++)
