@@ -128,6 +128,58 @@ def test_random_geometry(gpu, i):
     assert within(err, bar, "vs oracle")
 
 
+N_INT16 = 24
+
+
+@pytest.mark.parametrize("i", range(N_INT16))
+def test_random_geometry_int16(gpu, i):
+    """The INT16 way over int8 caches (blocks of up to 64 tokens, split-KV;
+    head sizes 64 to 512: the f16 planes' products at 64, the integer key
+    products from 128, the wide kernel at 512) against the restatement's
+    INT16 way, whose scores, weights and quantized weights are the
+    reference's bits: within the FLOAT bar (the sums differ only in order)."""
+    z = [int(x) for x in splitmix(7500 + i, 10)]
+    hd = [64, 128, 256, 512][z[0] % 4]
+    group = [1, 2, 4, 8][z[1] % 4]
+    n_kv = 1 + z[2] % 3
+    n = 1 + z[3] % 64
+    pos0 = z[4] % 3000
+    window = 0 if z[5] % 2 else 64 + z[6] % 1500
+    ring = window > 0 and z[7] % 3 == 0
+    cap = CHUNK * ((window + n) // CHUNK + 3) if ring else pos0 + n + z[8] % 200
+    g = dict(kv=KV_I8, hd=hd, n_head=group * n_kv, n_kv=n_kv, n=n, pos0=pos0,
+             window=window, ring=ring, gate=z[9] % 3, cap=cap, path="split",
+             seed=9700 + 10 * i)
+    print(f"case {i}: {g}", flush=True)
+    k, v, ks, vs, q, gate = inputs(g)
+    h = g["n_head"]
+    d = dict(k=to_dev(k, gpu), v=to_dev(v, gpu), ks=to_dev(ks, gpu), vs=to_dev(vs, gpu),
+             q=to_dev(q, gpu), out=torch.full((n, h, hd), float("nan"), device=gpu),
+             cap=cap, n=n, pos0=pos0)
+    gate_mode = 0
+    if gate is not None:
+        d["gate"] = to_dev(gate, gpu)
+        gate_mode = janas_amd.GATE_ELEM if g["gate"] == 1 else janas_amd.GATE_HEAD
+    with Attention(h, n_kv, hd, cap, 1, janas_amd.INT16) as a:
+        if window:
+            a.set_window(window)
+        if ring:
+            a.set_ring(True)
+        a.run_dev(KV_I8, [d], gate_mode=gate_mode, path="split")
+        torch.cuda.synchronize()
+    out = d["out"].cpu().numpy()
+    ref = orc.run(np.ascontiguousarray(q, np.float32), k, v, ks, vs, n_head=h,
+                  n_kv=n_kv, hd=hd, pos0=pos0, kv=KV_I8, window=window, ring=ring,
+                  threads=threads(), block=64, int16=True)
+    if gate is not None:
+        orc.gate(ref, gate, per_head=g["gate"] == 2)
+    assert np.isfinite(out).all()
+    err = abs_err(out, ref)
+    bar = TOL_FLOAT_ABS * max(1.0, float(np.abs(ref).max()))
+    print(f"case {i}: max err {err:.2e} (bar {bar:.1e})")
+    assert within(err, bar, "INT16 vs oracle")
+
+
 @pytest.mark.parametrize("path", ["split", "prefill"])
 def test_random_many_sequences(gpu, path):
     """19 sequences of random lengths and offsets in one call: the library
