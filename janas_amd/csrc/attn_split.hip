@@ -1059,6 +1059,19 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
         }
         mg = mb;
     }
+    /* the gate's sigmoid, made by group 0 while the other groups finish
+       (not after the barrier, on the way to the store) */
+    float sig[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; e++) {
+        sig[e] = 1.0f;
+        if (g == 0) {
+            if (A.gate_mode == kGateElem)
+                sig[e] = 1.0f / (1.0f + expf(-f4e(gv[e / 4], e % 4)));
+            else if (A.gate_mode == kGateHead)
+                sig[e] = 1.0f / (1.0f + expf(-gh));
+        }
+    }
     sM[g][cl] = mg;
     sL[g][cl] = lg;
 #pragma unroll
@@ -1111,10 +1124,8 @@ __global__ __launch_bounds__(256) void merge_kernel(const SplitArgs A)
                 x[k] = wk[k] * f4e(a, e % 4);
             }
             float y = (((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]))) * inv;
-            if (A.gate_mode == kGateElem)
-                y *= 1.0f / (1.0f + expf(-f4e(gv[e / 4], e % 4)));
-            else if (A.gate_mode == kGateHead)
-                y *= 1.0f / (1.0f + expf(-gh));
+            if (A.gate_mode != kGateNone)
+                y *= sig[e];
             f4e(o[e / 4], e % 4) = y;
             if constexpr (Q8K)
                 sOut[CPL * cl + e] = y;
