@@ -79,7 +79,10 @@ namespace {
  * 2 i is tile row i's high plane, 2 i + 1 its low plane, so a lane's two
  * neighbours hold one query row's two partial sums (added across lanes l
  * and l ^ 1 for the scores, and inside a lane for the values: output rows
- * 2 i and 2 i + 1 land in the same lane).
+ * 2 i and 2 i + 1 land in the same lane). The two lanes of a row split
+ * its work: lane l takes positions 2 (l & 1) and 2 (l & 1) + 1 of its four
+ * a group - their masks, softmax and both weight planes - and the pair
+ * swaps the plane each needs, so nothing is made twice.
  *
  *   S^T = K . Q^T   v_mfma_f32_16x16x32_f16 over the head dimension: A = a
  *                   group's 16 K rows (LDS), B = the query planes (LDS);
@@ -94,7 +97,9 @@ namespace {
  * score too), so every exponential is one v_exp_f32.
  *
  * Element types: f16 and int16 rows are staged as they are (int16 is split
- * into 256 (x >> 8) and x & 255 when read), int8 rows are widened to f16,
+ * into 256 (x >> 8) and x & 255 when read), int8 rows are widened to f16
+ * (the INT16 way's keys from head size 128 stay bytes, for the integer
+ * matrix cores),
  * f32 rows are split into two f16 planes; every LDS row is head size x 16
  * bits, its 16-byte units swizzled (unit u of row r in slot u ^ swz(r)) so
  * that both operand reads are free of bank conflicts.
@@ -456,7 +461,9 @@ __global__ __launch_bounds__(kSW * 64) __attribute__((amdgpu_waves_per_eu(D <= 1
                             (rlo[mt] <= p0w && p0w + kSWP - 1 <= rhi[mt]));
         full = __builtin_amdgcn_ballot_w64(!seen) == 0;
     }
-    float sv[MT][kSNG][4];
+    /* the scores of the lane's two positions of each group (its row's
+       other lane has the other two) */
+    float sv[MT][kSNG][2];
     float m[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
