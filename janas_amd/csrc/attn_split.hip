@@ -26,7 +26,7 @@
  *                  share an L2).
  *   merge kernel   one workgroup per (token, query head, 32 or 128 columns): the
  *                  ordered merge of the chunk partials (8 groups of chunks in
- *                  parallel, each in batches of 2, 4, 8 or 16 by the
+ *                  parallel, each in batches of 2 to 16 by the
  *                  launch's longest span, combined in a fixed
  *                  tree), the output gate sigmoid(g) * o (model_attn.c:
  *                  159-170) fused in.
@@ -933,7 +933,7 @@ __device__ __forceinline__ float &f4e(float4 &v, int e)
  * tokens), 1 when it has few (a decode spreads its loads over more CUs), 8
  * with Q8K.
  *
- * NB chunks a group's batch (2, 4, 8 or 16): every load of a batch is issued
+ * NB chunks a group's batch (2, 3, 4, 6, 8, 12 or 16): every load of a batch is issued
  * at once, and chunks past the row's range load its last chunk again and
  * enter with weight 0. Those are exact no-ops (the sums start at +0 and
  * never become -0, so adding 0 x v or 0 x l leaves them as they are), so
@@ -1292,10 +1292,16 @@ hipError_t launch_merge(const SplitArgs &a, uint32_t n_wg, hipStream_t s)
         span = a.seq[i].span > span ? a.seq[i].span : span;
     if (span <= kMergeGroups * 2)
         return launch_merge_nb<2>(a, n_wg, s);
+    if (span <= kMergeGroups * 3)
+        return launch_merge_nb<3>(a, n_wg, s);
     if (span <= kMergeGroups * 4)
         return launch_merge_nb<4>(a, n_wg, s);
+    if (span <= kMergeGroups * 6)
+        return launch_merge_nb<6>(a, n_wg, s);
     if (span <= kMergeGroups * 8)
         return launch_merge_nb<8>(a, n_wg, s);
+    if (span <= kMergeGroups * 12)
+        return launch_merge_nb<12>(a, n_wg, s);
     return launch_merge_nb<16>(a, n_wg, s);
 }
 
